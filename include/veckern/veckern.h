@@ -1,0 +1,149 @@
+/*
+ * veckern.h — C ABI of the MI355X (gfx950) PQ search library, libveckern.so.
+ *
+ * Plain C: pointers, sizes and integer status codes; no HIP, CUDA or C++ types. The C++ API of the reference
+ * (include/veckern/gpu.hpp: veckern::gpu::PQSearcher, ScanVariant, Tuning, DeviceInfo, Timings, LaunchShape)
+ * is implemented on top of these entry points by libveckern_gpu.so, and other languages bind them directly.
+ * Each declaration names the reference interface it replaces (paths relative to the reference checkout).
+ *
+ * Status: every int-returning call returns VK_OK or an error code; vk_last_error() then holds a message for
+ * the calling thread. The C++ layer rethrows VK_ERR_INVALID_ARGUMENT as std::invalid_argument, VK_ERR_LOGIC as
+ * std::logic_error and the others as std::runtime_error, the exception types the reference throws.
+ *
+ * Threading: a searcher owns one HIP stream and device buffers; calls on one searcher must not overlap.
+ * Every search call is synchronous. Results are deterministic.
+ */
+#ifndef VECKERN_H
+#define VECKERN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VK_ABI_VERSION 1
+
+enum vk_status {
+    VK_OK = 0,
+    VK_ERR_INVALID_ARGUMENT = 1, /* std::invalid_argument in the reference (searcher.cu:83, 89) */
+    VK_ERR_RUNTIME = 2,          /* std::runtime_error from check() (common.hpp:23-25) */
+    VK_ERR_LOGIC = 3,            /* std::logic_error (searcher.cu:281) */
+    VK_ERR_DEVICE = 4,           /* a HIP runtime call failed (the reference's VK_CUDA_CHECK, searcher.cu:11-16) */
+    VK_ERR_OUT_OF_MEMORY = 5     /* device allocation failed */
+};
+
+/* Scan variants: values and order of veckern::gpu::ScanVariant (gpu.hpp:13-23). */
+enum vk_variant {
+    VK_V0_GLOBAL_LUT = 0,
+    VK_V1_SHARED_LUT = 1,
+    VK_V2_SHARED_LUT_VEC = 2,
+    VK_V3_INTERLEAVED = 3,
+    VK_V4_FUSED = 4,
+    VK_V5_FUSED_REG = 5,
+    VK_V6_FUSED_VEC = 6,
+    VK_V7_FUSED_VEC_MQ = 7,
+    VK_V8_FUSED_WARP = 8,
+    VK_NUM_VARIANTS = 9
+};
+
+/* Same layout as veckern::Neighbor (common.hpp:13-16): ascending (dist, id); padding is {+inf, -1}. */
+typedef struct vk_neighbor {
+    float dist;
+    int32_t id;
+} vk_neighbor;
+
+/* veckern::gpu::Tuning (gpu.hpp:29-34); defaults {256, 0, 2, 4}. */
+typedef struct vk_tuning {
+    int scan_threads;      /* block size of the v0-v3 scans: multiple of 32 in [32, 1024] */
+    int blocks_per_query;  /* blocks per query (group) for scans and fused kernels; 0 = automatic */
+    int queries_per_block; /* Q for v7/v8: 1, 2, 4 or 8, lowered when the tables do not fit in LDS */
+    int vectors_per_step;  /* ILP for v6-v8: 1, 2 or 4 */
+} vk_tuning;
+
+/* veckern::gpu::Timings (gpu.hpp:46-50): milliseconds per stage from HIP events, summed over batches. */
+typedef struct vk_timings {
+    double transfer_ms, lut_ms, scan_ms, select_ms;
+} vk_timings;
+
+/* veckern::gpu::PQSearcher::LaunchShape (gpu.hpp:67-73): the shape the last search actually used. */
+typedef struct vk_launch_shape {
+    int threads, blocks_x, grid_y, queries_per_block, vectors_per_step;
+    int blocks_per_sm; /* occupancy-API residency (fused variants) */
+    double waves;      /* grid blocks / resident blocks */
+} vk_launch_shape;
+
+/* veckern::gpu::DeviceInfo (gpu.hpp:36-43), plus fields the MI355X reports need. */
+typedef struct vk_device_info {
+    char name[256];
+    char arch[64];              /* e.g. "gfx950:sramecc+:xnack-" */
+    int sm_count;               /* compute units */
+    double peak_bandwidth_gbs;  /* theoretical HBM bandwidth from memory clock and bus width */
+    size_t max_smem_per_block;  /* LDS bytes a block may use */
+    int clock_khz;
+    int warp_size;
+    size_t l2_bytes;
+    size_t total_mem_bytes;
+} vk_device_info;
+
+typedef struct vk_searcher vk_searcher;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* vk_last_error(void);
+int vk_abi_version(void);
+
+/* gpu.hpp:25 variant_name (names as searcher.cu:123-136), e.g. "v8_fused_warp"; "unknown" when out of range. */
+const char* vk_variant_name(int variant);
+/* gpu.hpp:26 is_fused (searcher.cu:138-141): 1 for v4-v8, 0 otherwise. */
+int vk_is_fused(int variant);
+/* Whether a variant needs m % 16 == 0 (bench_main.cpp:184-187; searcher.cu:243-246). */
+int vk_needs_m16(int variant);
+
+/* Host-only helpers (no device needed). */
+/* Tuning defaults of gpu.hpp:29-34. */
+void vk_tuning_default(vk_tuning* out);
+/* PQSearcher::set_tuning validation (searcher.cu:450-460): VK_OK or VK_ERR_RUNTIME with the reason. */
+int vk_tuning_validate(const vk_tuning* t);
+/* The list length K used for k (searcher.cu:86-90): smallest of 8, 16, 32, 64, 128 that is >= k;
+ * 0 with VK_ERR_INVALID_ARGUMENT when k > 128. */
+int vk_dispatched_k(size_t k);
+
+/* gpu.hpp:42 device_info(int device) (searcher.cu:143-156). */
+int vk_get_device_count(int* count);
+int vk_get_device_info(int device, vk_device_info* out);
+
+/* gpu.hpp:55 PQSearcher(pq, codes, n) (searcher.cu:427-444). centroids: [m][256][d/m] floats (pq.hpp:20-24);
+ * codes: row-major n x m bytes. Both are copied to the current device once; no host pointer is kept.
+ * Errors: d, m invalid or n == 0 or n >= INT32_MAX (VK_ERR_RUNTIME). */
+int vk_searcher_create(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n,
+                       vk_searcher** out);
+/* gpu.hpp:56 ~PQSearcher. Accepts NULL. */
+void vk_searcher_destroy(vk_searcher* s);
+/* gpu.hpp:63-64 set_tuning / tuning. */
+int vk_searcher_set_tuning(vk_searcher* s, const vk_tuning* t);
+int vk_searcher_get_tuning(const vk_searcher* s, vk_tuning* out);
+/* gpu.hpp:74 last_launch. */
+int vk_searcher_last_launch(const vk_searcher* s, vk_launch_shape* out);
+
+/* gpu.hpp:61 search (searcher.cu:466-520): out[nq * k] host memory, ascending (dist, id) per query, padded
+ * {+inf, -1}. Errors: k not in [1, min(128, n)] (VK_ERR_RUNTIME), m % 16 != 0 for v2/v6/v7/v8 or tables that
+ * do not fit in LDS (VK_ERR_RUNTIME). timings may be NULL. nq == 0 is a no-op. */
+int vk_search(vk_searcher* s, const float* queries, size_t nq, size_t k, int variant, vk_neighbor* out,
+              vk_timings* timings);
+/* gpu.hpp:62 distances (searcher.cu:522-547): out[nq * n] host memory of ADC distances; v0-v3 only
+ * (VK_ERR_RUNTIME for fused variants, as check() in the reference). */
+int vk_distances(vk_searcher* s, const float* queries, size_t nq, int variant, float* out, vk_timings* timings);
+
+/* Device-resident search: same as vk_search, but d_queries (nq x d floats) and d_out (nq x k vk_neighbor) are
+ * device pointers on the searcher's device, so no PCIe transfer is made or timed (transfer_ms = 0). This is the
+ * entry a caller whose data already lives in HBM uses. No counterpart in the reference, which always copies
+ * queries in and results out. */
+int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq, size_t k, int variant, vk_neighbor* d_out,
+                     vk_timings* timings);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VECKERN_H */

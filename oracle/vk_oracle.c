@@ -1,0 +1,204 @@
+/*
+ * vk_oracle — CPU restatement of VecKern's PQ search path. TEST INFRASTRUCTURE ONLY: the checker for the GPU
+ * path, never part of it. The reference line each function follows is cited in vk_oracle.h and below.
+ */
+#include "vk_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* common.hpp:19-21 — strict order by (dist, id), so CPU and GPU break distance ties by id. */
+int vko_less(float ad, int32_t ai, float bd, int32_t bi) { return ad < bd || (ad == bd && ai < bi); }
+
+/* common.hpp:27-34 — squared L2 with a single accumulator, terms added in index order. */
+float vko_l2sq(const float* a, const float* b, size_t d) {
+    float acc = 0.f;
+    for (size_t j = 0; j < d; ++j) {
+        const float diff = a[j] - b[j];
+        acc += diff * diff;
+    }
+    return acc;
+}
+
+/* ---- bounded top-k (cpu_ref.hpp:14-40). A binary max-heap under vko_less holds the k best seen so far;
+ * the root is the worst of them, so a new pair enters only if it is strictly better than the root. */
+
+static int nb_less(const vko_neighbor* a, const vko_neighbor* b) { return vko_less(a->dist, a->id, b->dist, b->id); }
+
+static void swap_nb(vko_neighbor* a, vko_neighbor* b) {
+    const vko_neighbor t = *a;
+    *a = *b;
+    *b = t;
+}
+
+static void sift_down(vko_neighbor* h, size_t size, size_t i) {
+    for (;;) {
+        const size_t l = 2 * i + 1, r = l + 1;
+        size_t big = i;
+        if (l < size && nb_less(&h[big], &h[l])) big = l;
+        if (r < size && nb_less(&h[big], &h[r])) big = r;
+        if (big == i) return;
+        swap_nb(&h[i], &h[big]);
+        i = big;
+    }
+}
+
+static void sift_up(vko_neighbor* h, size_t i) {
+    while (i > 0) {
+        const size_t p = (i - 1) / 2;
+        if (!nb_less(&h[p], &h[i])) return;
+        swap_nb(&h[p], &h[i]);
+        i = p;
+    }
+}
+
+int vko_topk_init(vko_topk* t, size_t k) {
+    t->k = k;
+    t->size = 0;
+    t->heap = k ? (vko_neighbor*)malloc(k * sizeof(vko_neighbor)) : NULL;
+    return (k == 0 || t->heap) ? 0 : -1;
+}
+
+void vko_topk_free(vko_topk* t) {
+    free(t->heap);
+    t->heap = NULL;
+    t->size = t->k = 0;
+}
+
+void vko_topk_push(vko_topk* t, float dist, int32_t id) {
+    const vko_neighbor cand = {dist, id};
+    if (t->size < t->k) {
+        t->heap[t->size] = cand;
+        sift_up(t->heap, t->size);
+        ++t->size;
+    } else if (t->k > 0 && nb_less(&cand, &t->heap[0])) {
+        t->heap[0] = cand;
+        sift_down(t->heap, t->size, 0);
+    }
+}
+
+void vko_topk_write(vko_topk* t, vko_neighbor* out) {
+    /* heapsort in place: the root (largest) goes to the end each round, giving ascending order */
+    for (size_t end = t->size; end > 1; --end) {
+        swap_nb(&t->heap[0], &t->heap[end - 1]);
+        sift_down(t->heap, end - 1, 0);
+    }
+    for (size_t j = 0; j < t->size; ++j) out[j] = t->heap[j];
+    for (size_t j = t->size; j < t->k; ++j) {
+        out[j].dist = INFINITY;
+        out[j].id = -1;
+    }
+    t->size = 0;
+}
+
+/* ---- cpu_ref.cpp:7-14. Centroid (s, c) starts at centroids + (s * 256 + c) * dsub (pq.hpp:20-24). */
+void vko_compute_lut(const float* centroids, size_t d, size_t m, const float* queries, size_t nq, float* lut) {
+    const size_t dsub = d / m;
+#pragma omp parallel for schedule(static)
+    for (long long q = 0; q < (long long)nq; ++q)
+        for (size_t s = 0; s < m; ++s)
+            for (size_t c = 0; c < VKO_KSUB; ++c)
+                lut[((size_t)q * m + s) * VKO_KSUB + c] =
+                    vko_l2sq(queries + (size_t)q * d + s * dsub, centroids + (s * VKO_KSUB + c) * dsub, dsub);
+}
+
+/* ---- cpu_ref.cpp:16-27: the distance of vector i is summed over s = 0..m-1 starting from 0.f. */
+void vko_adc_scan(const float* lut, size_t nq, const uint8_t* codes, size_t n, size_t m, float* dists) {
+#pragma omp parallel for schedule(static)
+    for (long long q = 0; q < (long long)nq; ++q) {
+        const float* table = lut + (size_t)q * m * VKO_KSUB;
+        for (size_t i = 0; i < n; ++i) {
+            const uint8_t* code = codes + i * m;
+            float acc = 0.f;
+            for (size_t s = 0; s < m; ++s) acc += table[s * VKO_KSUB + code[s]];
+            dists[(size_t)q * n + i] = acc;
+        }
+    }
+}
+
+/* ---- cpu_ref.cpp:29-36 */
+void vko_select_topk(const float* dists, size_t nq, size_t n, size_t k, vko_neighbor* out) {
+#pragma omp parallel for schedule(static)
+    for (long long q = 0; q < (long long)nq; ++q) {
+        vko_topk top;
+        if (vko_topk_init(&top, k) != 0) continue;
+        for (size_t i = 0; i < n; ++i) vko_topk_push(&top, dists[(size_t)q * n + i], (int32_t)i);
+        vko_topk_write(&top, out + (size_t)q * k);
+        vko_topk_free(&top);
+    }
+}
+
+/* ---- cpu_ref.cpp:38-54: one query at a time (dynamic schedule), its own LUT, sequential scan, heap. */
+int vko_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n, const float* queries,
+                   size_t nq, size_t k, vko_neighbor* out) {
+    if (m == 0 || d == 0 || d % m != 0) return -1;
+    int failed = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (long long q = 0; q < (long long)nq; ++q) {
+        float* lut = (float*)malloc(m * VKO_KSUB * sizeof(float));
+        vko_topk top;
+        if (!lut || vko_topk_init(&top, k) != 0) {
+            free(lut);
+            failed = 1;
+            continue;
+        }
+        const float* x = queries + (size_t)q * d;
+        const size_t dsub = d / m;
+        for (size_t s = 0; s < m; ++s)
+            for (size_t c = 0; c < VKO_KSUB; ++c)
+                lut[s * VKO_KSUB + c] = vko_l2sq(x + s * dsub, centroids + (s * VKO_KSUB + c) * dsub, dsub);
+        for (size_t i = 0; i < n; ++i) {
+            const uint8_t* code = codes + i * m;
+            float acc = 0.f;
+            for (size_t s = 0; s < m; ++s) acc += lut[s * VKO_KSUB + code[s]];
+            vko_topk_push(&top, acc, (int32_t)i);
+        }
+        vko_topk_write(&top, out + (size_t)q * k);
+        vko_topk_free(&top);
+        free(lut);
+    }
+    return failed ? -1 : 0;
+}
+
+/* ---- cpu_ref.cpp:79-91: truth[:k] is treated as a set; every found id that is in it counts as a hit. */
+double vko_recall_at_k(const vko_neighbor* found, size_t found_stride, const int32_t* truth, size_t truth_stride,
+                       size_t nq, size_t k) {
+    if (k > found_stride || k > truth_stride) return -1.0;
+    if (nq == 0 || k == 0) return 0.0;
+    double total = 0.0;
+    for (size_t q = 0; q < nq; ++q) {
+        const int32_t* t = truth + q * truth_stride;
+        size_t hits = 0;
+        for (size_t j = 0; j < k; ++j) {
+            const int32_t id = found[q * found_stride + j].id;
+            for (size_t u = 0; u < k; ++u)
+                if (t[u] == id) {
+                    ++hits;
+                    break;
+                }
+        }
+        total += (double)hits / (double)k;
+    }
+    return total / (double)nq;
+}
+
+void vko_topk_run(const float* dists, const int32_t* ids, size_t count, size_t k, vko_neighbor* out) {
+    vko_topk top;
+    if (vko_topk_init(&top, k) != 0) return;
+    for (size_t j = 0; j < count; ++j) vko_topk_push(&top, dists[j], ids[j]);
+    vko_topk_write(&top, out);
+    vko_topk_free(&top);
+}
+
+int vko_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

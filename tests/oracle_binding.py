@@ -1,0 +1,130 @@
+"""ctypes binding of the oracle (oracle/lib/libvk_oracle.so) and, when built, of the reference's own CPU library
+(oracle/_ref/libvkref.so). Test infrastructure: these are the checkers the GPU path is compared against.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_LIB = os.path.join(ROOT, "oracle", "lib", "libvk_oracle.so")
+REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libvkref.so")
+
+NEIGHBOR = np.dtype([("dist", np.float32), ("id", np.int32)])
+_P = ctypes.c_void_p
+_S = ctypes.c_size_t
+
+_oracle = None
+_ref = None
+
+
+def oracle() -> ctypes.CDLL:
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_LIB):
+            raise RuntimeError(f"{ORACLE_LIB} missing: run `make -C oracle`")
+        lib = ctypes.CDLL(ORACLE_LIB)
+        lib.vko_less.argtypes = [ctypes.c_float, ctypes.c_int32, ctypes.c_float, ctypes.c_int32]
+        lib.vko_l2sq.restype = ctypes.c_float
+        lib.vko_l2sq.argtypes = [_P, _P, _S]
+        lib.vko_compute_lut.argtypes = [_P, _S, _S, _P, _S, _P]
+        lib.vko_adc_scan.argtypes = [_P, _S, _P, _S, _S, _P]
+        lib.vko_select_topk.argtypes = [_P, _S, _S, _S, _P]
+        lib.vko_adc_search.argtypes = [_P, _S, _S, _P, _S, _P, _S, _S, _P]
+        lib.vko_recall_at_k.restype = ctypes.c_double
+        lib.vko_recall_at_k.argtypes = [_P, _S, _P, _S, _S, _S]
+        lib.vko_max_threads.restype = ctypes.c_int
+        lib.vko_topk_run.argtypes = [_P, _P, _S, _S, _P]
+        _oracle = lib
+    return _oracle
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_LIB)
+
+
+def ref() -> ctypes.CDLL:
+    global _ref
+    if _ref is None:
+        lib = ctypes.CDLL(REF_LIB)
+        lib.vkref_pq_create.restype = _P
+        lib.vkref_pq_create.argtypes = [_S, _S]
+        lib.vkref_pq_destroy.argtypes = [_P]
+        lib.vkref_pq_train.argtypes = [_P, _P, _S, _S, ctypes.c_uint64]
+        lib.vkref_pq_encode.argtypes = [_P, _P, _S, _P]
+        lib.vkref_pq_decode.argtypes = [_P, _P, _S, _P]
+        lib.vkref_pq_centroids.argtypes = [_P, _P]
+        lib.vkref_compute_lut.argtypes = [_P, _P, _S, _P]
+        lib.vkref_adc_scan.argtypes = [_P, _S, _P, _S, _S, _P]
+        lib.vkref_select_topk.argtypes = [_P, _S, _S, _S, _P]
+        lib.vkref_adc_search.argtypes = [_P, _P, _S, _P, _S, _S, _P]
+        lib.vkref_exact_knn.argtypes = [_P, _S, _P, _S, _S, _S, _P]
+        lib.vkref_recall_at_k.restype = ctypes.c_double
+        lib.vkref_recall_at_k.argtypes = [_P, _S, _P, _S, _S, _S]
+        lib.vkref_topk_run.argtypes = [_P, _P, _S, _S, _P]
+        lib.vkref_synthetic_clustered.argtypes = [_S, _S, _S, ctypes.c_uint64, _P]
+        _ref = lib
+    return _ref
+
+
+def _c(a: np.ndarray, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- oracle wrappers
+
+def compute_lut(centroids: np.ndarray, d: int, m: int, queries: np.ndarray) -> np.ndarray:
+    q = _c(queries, np.float32).reshape(-1, d)
+    c = _c(centroids, np.float32)
+    lut = np.empty((q.shape[0], m, 256), dtype=np.float32)
+    oracle().vko_compute_lut(c.ctypes.data, d, m, q.ctypes.data, q.shape[0], lut.ctypes.data)
+    return lut
+
+
+def adc_scan(lut: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    lut = _c(lut, np.float32)
+    codes = _c(codes, np.uint8)
+    n, m = codes.shape
+    nq = lut.size // (m * 256)
+    out = np.empty((nq, n), dtype=np.float32)
+    oracle().vko_adc_scan(lut.ctypes.data, nq, codes.ctypes.data, n, m, out.ctypes.data)
+    return out
+
+
+def select_topk(dists: np.ndarray, k: int) -> np.ndarray:
+    dists = _c(dists, np.float32)
+    nq, n = dists.shape
+    out = np.empty((nq, k), dtype=NEIGHBOR)
+    oracle().vko_select_topk(dists.ctypes.data, nq, n, k, out.ctypes.data)
+    return out
+
+
+def adc_search(centroids: np.ndarray, d: int, codes: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
+    codes = _c(codes, np.uint8)
+    n, m = codes.shape
+    q = _c(queries, np.float32).reshape(-1, d)
+    c = _c(centroids, np.float32)
+    out = np.empty((q.shape[0], k), dtype=NEIGHBOR)
+    rc = oracle().vko_adc_search(c.ctypes.data, d, m, codes.ctypes.data, n, q.ctypes.data, q.shape[0], k,
+                                 out.ctypes.data)
+    if rc != 0:
+        raise ValueError("vko_adc_search rejected its input")
+    return out
+
+
+def recall_at_k(found: np.ndarray, truth: np.ndarray, k: int) -> float:
+    found = _c(found, NEIGHBOR)
+    truth = _c(truth, np.int32)
+    return oracle().vko_recall_at_k(found.ctypes.data, found.shape[1], truth.ctypes.data, truth.shape[1],
+                                    found.shape[0], k)
+
+
+def topk_run(dists, ids, k: int, use_ref: bool = False) -> np.ndarray:
+    d = _c(dists, np.float32)
+    i = _c(ids, np.int32)
+    out = np.empty(k, dtype=NEIGHBOR)
+    fn = ref().vkref_topk_run if use_ref else oracle().vko_topk_run
+    fn(d.ctypes.data, i.ctypes.data, d.size, k, out.ctypes.data)
+    return out

@@ -1,0 +1,492 @@
+// C ABI of libveckern.so: device buffers, code layouts, launch planning, query batching and per-stage HIP-event
+// timing for every scan variant. Host orchestration counterpart of the reference's src/cuda/searcher.cu, written
+// for one MI355X: persistent balanced grids sized by the occupancy API, query-interleaved LDS tables, and
+// wave64 code tiles.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "planning.hpp"
+#include "veckern/veckern.h"
+
+#define VK_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace vk {
+// Per-m instance tables of the wave-list scan (fused_wave_m*.hip).
+WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_m64(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments);
+
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments) {
+    switch (m) {
+        case 16: return fused_wave_kernel_m16(qg, ng, ilp, segments);
+        case 32: return fused_wave_kernel_m32(qg, ng, ilp, segments);
+        case 64: return fused_wave_kernel_m64(qg, ng, ilp, segments);
+        default: return fused_wave_kernel_mx(qg, ng, ilp, segments);
+    }
+}
+}  // namespace vk
+
+namespace {
+
+using vk::Pair;
+
+thread_local std::string g_error;
+
+struct Failure {
+    int code;
+    std::string message;
+};
+
+[[noreturn]] void fail(int code, const std::string& message) { throw Failure{code, message}; }
+
+void require(bool condition, const std::string& message) {
+    if (!condition) fail(VK_ERR_RUNTIME, message);
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        fail(e == hipErrorOutOfMemory ? VK_ERR_OUT_OF_MEMORY : VK_ERR_DEVICE,
+             std::string(what) + " failed: " + hipGetErrorString(e));
+}
+#define VK_HIP(call) hip_check((call), #call)
+
+template <typename F>
+int guarded(F&& body) {
+    try {
+        body();
+        g_error.clear();
+        return VK_OK;
+    } catch (const Failure& f) {
+        g_error = f.message;
+        return f.code;
+    } catch (const std::bad_alloc&) {
+        g_error = "host allocation failed";
+        return VK_ERR_OUT_OF_MEMORY;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return VK_ERR_RUNTIME;
+    } catch (...) {
+        g_error = "unknown error";
+        return VK_ERR_RUNTIME;
+    }
+}
+
+template <typename T>
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer() { release(); }
+    void ensure(size_t count) {
+        if (count <= capacity_) return;
+        release();
+        void* p = nullptr;
+        VK_HIP(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)));
+        ptr_ = static_cast<T*>(p);
+        capacity_ = count;
+    }
+    void release() {
+        if (ptr_) (void)hipFree(ptr_);
+        ptr_ = nullptr;
+        capacity_ = 0;
+    }
+    T* get() const { return ptr_; }
+    bool empty() const { return ptr_ == nullptr; }
+
+private:
+    T* ptr_ = nullptr;
+    size_t capacity_ = 0;
+};
+
+// Event pairs recorded around the stages of one batch; read after the batch's final synchronisation.
+class StageClock {
+public:
+    explicit StageClock(hipStream_t stream) : stream_(stream) {}
+    ~StageClock() {
+        for (auto& e : events_) (void)hipEventDestroy(e);
+    }
+    template <typename F>
+    void time(double* acc, F&& work) {
+        hipEvent_t a = next(), b = next();
+        VK_HIP(hipEventRecord(a, stream_));
+        work();
+        VK_HIP(hipEventRecord(b, stream_));
+        pending_.push_back({a, b, acc});
+    }
+    // Waits for the stream and adds every pending stage's elapsed time to its accumulator.
+    void settle() {
+        VK_HIP(hipStreamSynchronize(stream_));
+        for (const auto& p : pending_) {
+            float ms = 0.f;
+            VK_HIP(hipEventElapsedTime(&ms, p.start, p.stop));
+            *p.acc += ms;
+        }
+        pending_.clear();
+        used_ = 0;
+    }
+
+private:
+    struct Pending {
+        hipEvent_t start, stop;
+        double* acc;
+    };
+    hipEvent_t next() {
+        if (used_ == events_.size()) {
+            hipEvent_t e;
+            VK_HIP(hipEventCreate(&e));
+            events_.push_back(e);
+        }
+        return events_[used_++];
+    }
+    hipStream_t stream_;
+    std::vector<hipEvent_t> events_;
+    std::vector<Pending> pending_;
+    size_t used_ = 0;
+};
+
+bool valid_variant(int v) { return v >= 0 && v < VK_NUM_VARIANTS; }
+
+void fill_device_info(int device, vk_device_info* out) {
+    hipDeviceProp_t p{};
+    VK_HIP(hipGetDeviceProperties(&p, device));
+    std::memset(out, 0, sizeof(*out));
+    std::snprintf(out->name, sizeof(out->name), "%s", p.name[0] ? p.name : "AMD Instinct GPU");
+    std::snprintf(out->arch, sizeof(out->arch), "%s", p.gcnArchName);
+    out->sm_count = p.multiProcessorCount;
+    // HBM3/HBM3E: the runtime reports the memory clock at a quarter of the per-pin data rate, so the peak is
+    // 4 transfers per reported clock over the full bus (MI355X: 2.0 GHz x 4 x 8192 bits / 8 = 8.19 TB/s).
+    out->peak_bandwidth_gbs = 4.0 * p.memoryClockRate * 1e3 * (p.memoryBusWidth / 8.0) / 1e9;
+    out->max_smem_per_block = p.sharedMemPerBlock;
+    out->clock_khz = p.clockRate;
+    out->warp_size = p.warpSize;
+    out->l2_bytes = static_cast<size_t>(p.l2CacheSize);
+    out->total_mem_bytes = p.totalGlobalMem;
+}
+
+}  // namespace
+
+struct vk_searcher {
+    int device = 0;
+    size_t n = 0, d = 0, m = 0;
+    int64_t n_pad = 0;  // n rounded up to 256 vectors: every wave step of up to 4 tiles stays in bounds
+    vk_device_info info{};
+    vk_tuning tuning{};
+    vk_launch_shape last{};
+    hipStream_t stream = nullptr;
+    DeviceBuffer<float> centroids, queries, lut, dists;
+    DeviceBuffer<uint8_t> codes, codes_il;
+    DeviceBuffer<uint4> codes_v;
+    DeviceBuffer<Pair> part, out;
+    bool have_il = false, have_v = false;
+
+    ~vk_searcher() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    void use_device() const { VK_HIP(hipSetDevice(device)); }
+
+    void validate(int v) const {
+        if (vk_needs_m16(v)) require(m % 16 == 0, std::string(vk_variant_name(v)) + " requires m % 16 == 0");
+        if (v != VK_V0_GLOBAL_LUT)
+            require(m * vk::KSUB * sizeof(float) <= info.max_smem_per_block, "LUT does not fit in LDS");
+    }
+
+    void ensure_layout(int v) {
+        if (vk::plan::uses_byte_layout(v) && !have_il) {
+            codes_il.ensure(static_cast<size_t>(n_pad) * m);
+            VK_HIP(vk::launch_build_bytes(codes.get(), n, static_cast<int>(m), n_pad, codes_il.get(), stream));
+            have_il = true;
+        }
+        if (vk::plan::uses_word_layout(v) && !have_v) {
+            codes_v.ensure(static_cast<size_t>(n_pad) * (m / 16));
+            VK_HIP(vk::launch_build_words(codes.get(), n, static_cast<int>(m), n_pad, codes_v.get(), stream));
+            have_v = true;
+        }
+        VK_HIP(hipStreamSynchronize(stream));
+    }
+
+    // v8: the wave-list scan over the balanced partition, then the final merge. d_q: device queries of this
+    // batch; writes b x kk results to d_out.
+    void run_wave(const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
+        const int K = vk::plan::dispatched_k(kk);
+        const int segments = K <= vk::WAVE ? 1 : 2;
+        const int q = vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, false, K);
+        const int qg = q == 8 ? 4 : q, ng = q == 8 ? 2 : 1;
+        const int ilp = tuning.vectors_per_step;
+        const vk::WaveScanKernel kern = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments);
+        if (!kern.fn) fail(VK_ERR_LOGIC, "no fused-warp kernel built for this (Q, ILP, m, K)");
+        const size_t tables = static_cast<size_t>(q) * m * vk::KSUB * sizeof(float);
+        require(tables <= info.max_smem_per_block, "LUT does not fit in LDS");
+        const size_t smem = kern.dynamic_lds ? tables : 0;  // fixed-m instances hold the tables in static LDS
+        if (kern.dynamic_lds)
+            VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+        int per_cu = 0;
+        VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
+        per_cu = std::max(per_cu, 1);
+
+        const vk::plan::Partition part_plan = vk::plan::balanced_partition(
+            static_cast<int64_t>(n), b, q, ilp, static_cast<int64_t>(per_cu) * info.sm_count, tuning.blocks_per_query);
+        const size_t groups = static_cast<size_t>(part_plan.slabs) * ng;
+        lut.ensure(groups * qg * m * vk::KSUB);
+        part.ensure(static_cast<size_t>(part_plan.slabs) * part_plan.max_slots * q * K);
+
+        last = vk_launch_shape{};
+        last.threads = kern.threads;
+        last.blocks_x = static_cast<int>(part_plan.grid);
+        last.grid_y = 1;
+        last.queries_per_block = q;
+        last.vectors_per_step = ilp;
+        last.blocks_per_sm = per_cu;
+        last.waves = static_cast<double>(part_plan.grid) / (static_cast<double>(per_cu) * info.sm_count);
+
+        clock.time(&t->lut_ms, [&] {
+            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(b),
+                                  qg, static_cast<int>(groups), lut.get(), stream));
+        });
+        vk::WaveScanArgs a{};
+        a.lut = lut.get();
+        a.codes = codes_v.get();
+        a.n = static_cast<int64_t>(n);
+        a.m = static_cast<int>(m);
+        a.nq = static_cast<int>(b);
+        a.K = K;
+        a.n_gran = part_plan.n_gran;
+        a.total = part_plan.total;
+        a.max_slots = part_plan.max_slots;
+        a.part = part.get();
+        clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(part_plan.grid), smem, stream)); });
+
+        vk::SelectArgs s{};
+        s.mode = 2;
+        s.part = part.get();
+        s.K = K;
+        s.qs = q;
+        s.max_slots = part_plan.max_slots;
+        s.n_gran = part_plan.n_gran;
+        s.total = part_plan.total;
+        s.grid = part_plan.grid;
+        s.k = static_cast<int>(kk);
+        s.out = d_out;
+        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
+    }
+
+    void run_variant(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
+        if (v == VK_V8_FUSED_WARP) return run_wave(d_q, b, kk, d_out, t, clock);
+        fail(VK_ERR_LOGIC, std::string(vk_variant_name(v)) + " is not available in this build");
+    }
+
+    void check_search(size_t kk, int v) const {
+        require(valid_variant(v), "unknown scan variant " + std::to_string(v));
+        require(kk >= 1 && kk <= 128 && kk <= n, "k must be in [1, min(128, n)]");
+        validate(v);
+    }
+
+    // Queries per launch batch: bounded so the LUT buffer stays under 1 GiB.
+    size_t query_batch() const {
+        const size_t per_query = m * vk::KSUB * sizeof(float);
+        return std::max<size_t>(1, std::min<size_t>(65536, (size_t{1} << 30) / per_query));
+    }
+
+    void search_host(const float* host_q, size_t nq, size_t kk, int v, vk_neighbor* host_out, vk_timings* t) {
+        check_search(kk, v);
+        use_device();
+        ensure_layout(v);
+        StageClock clock(stream);
+        const size_t batch = query_batch();
+        for (size_t q0 = 0; q0 < nq; q0 += batch) {
+            const size_t b = std::min(batch, nq - q0);
+            queries.ensure(b * d);
+            out.ensure(b * kk);
+            clock.time(&t->transfer_ms, [&] {
+                VK_HIP(hipMemcpyAsync(queries.get(), host_q + q0 * d, b * d * sizeof(float), hipMemcpyHostToDevice,
+                                      stream));
+            });
+            run_variant(v, queries.get(), b, kk, out.get(), t, clock);
+            clock.time(&t->transfer_ms, [&] {
+                VK_HIP(hipMemcpyAsync(host_out + q0 * kk, out.get(), b * kk * sizeof(Pair), hipMemcpyDeviceToHost,
+                                      stream));
+            });
+            clock.settle();
+        }
+    }
+
+    void search_device(const float* d_q, size_t nq, size_t kk, int v, vk_neighbor* d_out, vk_timings* t) {
+        check_search(kk, v);
+        use_device();
+        ensure_layout(v);
+        StageClock clock(stream);
+        const size_t batch = query_batch();
+        for (size_t q0 = 0; q0 < nq; q0 += batch) {
+            const size_t b = std::min(batch, nq - q0);
+            run_variant(v, d_q + q0 * d, b, kk, reinterpret_cast<Pair*>(d_out + q0 * kk), t, clock);
+            clock.settle();
+        }
+    }
+};
+
+static_assert(sizeof(vk_neighbor) == sizeof(Pair), "vk_neighbor and the device pair must share a layout");
+
+// ------------------------------------------------------------------------------------------------ exports
+
+VK_EXPORT const char* vk_last_error(void) { return g_error.c_str(); }
+VK_EXPORT int vk_abi_version(void) { return VK_ABI_VERSION; }
+
+VK_EXPORT const char* vk_variant_name(int v) {
+    static const char* const names[VK_NUM_VARIANTS] = {"v0_global_lut", "v1_shared_lut", "v2_shared_lut_vec",
+                                                       "v3_interleaved", "v4_fused",      "v5_fused_reg",
+                                                       "v6_fused_vec",  "v7_fused_vec_mq", "v8_fused_warp"};
+    return valid_variant(v) ? names[v] : "unknown";
+}
+
+VK_EXPORT int vk_is_fused(int v) { return v >= VK_V4_FUSED && v <= VK_V8_FUSED_WARP; }
+
+VK_EXPORT int vk_needs_m16(int v) {
+    return v == VK_V2_SHARED_LUT_VEC || v == VK_V6_FUSED_VEC || v == VK_V7_FUSED_VEC_MQ || v == VK_V8_FUSED_WARP;
+}
+
+VK_EXPORT void vk_tuning_default(vk_tuning* out) {
+    if (out) *out = vk_tuning{256, 0, 2, 4};
+}
+
+VK_EXPORT int vk_tuning_validate(const vk_tuning* t) {
+    return guarded([&] {
+        require(t != nullptr, "tuning is null");
+        require(t->scan_threads >= 32 && t->scan_threads <= 1024 && t->scan_threads % 32 == 0,
+                "scan_threads must be a multiple of 32 in [32, 1024]");
+        require(t->blocks_per_query >= 0, "blocks_per_query must be >= 0");
+        require(t->queries_per_block == 1 || t->queries_per_block == 2 || t->queries_per_block == 4 ||
+                    t->queries_per_block == 8,
+                "queries_per_block must be 1, 2, 4 or 8");
+        require(t->vectors_per_step == 1 || t->vectors_per_step == 2 || t->vectors_per_step == 4,
+                "vectors_per_step must be 1, 2 or 4");
+    });
+}
+
+VK_EXPORT int vk_dispatched_k(size_t k) {
+    const int K = vk::plan::dispatched_k(k);
+    if (K == 0) {
+        g_error = "k must be <= 128";
+        return 0;
+    }
+    return K;
+}
+
+VK_EXPORT int vk_get_device_count(int* count) {
+    return guarded([&] {
+        require(count != nullptr, "count is null");
+        VK_HIP(hipGetDeviceCount(count));
+    });
+}
+
+VK_EXPORT int vk_get_device_info(int device, vk_device_info* out) {
+    return guarded([&] {
+        require(out != nullptr, "out is null");
+        fill_device_info(device, out);
+    });
+}
+
+VK_EXPORT int vk_searcher_create(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n,
+                                 vk_searcher** out) {
+    return guarded([&] {
+        require(out != nullptr, "out is null");
+        *out = nullptr;
+        require(m > 0 && d > 0 && d % m == 0, "d must be a positive multiple of m");
+        require(n > 0 && n < static_cast<size_t>(std::numeric_limits<int32_t>::max()), "n must fit in int32 ids");
+        require(centroids != nullptr && codes != nullptr, "centroids and codes must not be null");
+        auto s = std::make_unique<vk_searcher>();
+        VK_HIP(hipGetDevice(&s->device));
+        fill_device_info(s->device, &s->info);
+        vk_tuning_default(&s->tuning);
+        s->n = n;
+        s->d = d;
+        s->m = m;
+        s->n_pad = static_cast<int64_t>((n + 255) / 256 * 256);
+        VK_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+        s->centroids.ensure(m * vk::KSUB * (d / m));
+        VK_HIP(hipMemcpy(s->centroids.get(), centroids, m * vk::KSUB * (d / m) * sizeof(float), hipMemcpyHostToDevice));
+        s->codes.ensure(n * m);
+        VK_HIP(hipMemcpy(s->codes.get(), codes, n * m, hipMemcpyHostToDevice));
+        *out = s.release();
+    });
+}
+
+VK_EXPORT void vk_searcher_destroy(vk_searcher* s) { delete s; }
+
+VK_EXPORT int vk_searcher_set_tuning(vk_searcher* s, const vk_tuning* t) {
+    return guarded([&] {
+        require(s != nullptr, "searcher is null");
+        const int rc = vk_tuning_validate(t);
+        if (rc != VK_OK) fail(rc, g_error);
+        s->tuning = *t;
+    });
+}
+
+VK_EXPORT int vk_searcher_get_tuning(const vk_searcher* s, vk_tuning* out) {
+    return guarded([&] {
+        require(s != nullptr && out != nullptr, "null argument");
+        *out = s->tuning;
+    });
+}
+
+VK_EXPORT int vk_searcher_last_launch(const vk_searcher* s, vk_launch_shape* out) {
+    return guarded([&] {
+        require(s != nullptr && out != nullptr, "null argument");
+        *out = s->last;
+    });
+}
+
+VK_EXPORT int vk_search(vk_searcher* s, const float* queries, size_t nq, size_t k, int variant, vk_neighbor* out,
+                        vk_timings* timings) {
+    return guarded([&] {
+        require(s != nullptr, "searcher is null");
+        vk_timings t{};
+        if (nq > 0) {
+            require(queries != nullptr && out != nullptr, "queries and out must not be null");
+            s->search_host(queries, nq, k, variant, out, &t);
+        } else {
+            s->check_search(k, variant);
+        }
+        if (timings) *timings = t;
+    });
+}
+
+VK_EXPORT int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq, size_t k, int variant,
+                               vk_neighbor* d_out, vk_timings* timings) {
+    return guarded([&] {
+        require(s != nullptr, "searcher is null");
+        vk_timings t{};
+        if (nq > 0) {
+            require(d_queries != nullptr && d_out != nullptr, "queries and out must not be null");
+            s->search_device(d_queries, nq, k, variant, d_out, &t);
+        } else {
+            s->check_search(k, variant);
+        }
+        if (timings) *timings = t;
+    });
+}
+
+VK_EXPORT int vk_distances(vk_searcher* s, const float* queries, size_t nq, int variant, float* out,
+                           vk_timings* timings) {
+    return guarded([&] {
+        require(s != nullptr, "searcher is null");
+        require(valid_variant(variant), "unknown scan variant");
+        require(!vk_is_fused(variant), "fused variants do not materialise distances");
+        fail(VK_ERR_LOGIC, "distances() is not available in this build");
+        (void)queries;
+        (void)nq;
+        (void)out;
+        (void)timings;
+    });
+}

@@ -1,0 +1,154 @@
+// Device building blocks shared by the gfx950 kernels: result ordering, the empty-slot sentinel, and the
+// wave64-cooperative sorted top-k list.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+
+namespace vk {
+
+constexpr int KSUB = 256;  // centroids per sub-space: one byte per sub-code
+constexpr int WAVE = 64;   // CDNA wavefront width
+
+// An empty list slot is (+inf, INT32_MAX). It sorts after every real candidate, including one whose distance
+// overflowed to +inf, so lists stay exact under the total order and the host turns surviving empty slots into
+// the reference's {+inf, -1} padding (searcher.cu:514-517).
+constexpr int32_t kEmptyId = INT32_MAX;
+
+struct alignas(8) Pair {
+    float d;
+    int32_t i;
+};
+
+// Total order by (distance, id): common.hpp:19-21 / kernels.cuh:116.
+__device__ __forceinline__ bool pair_less(float ad, int32_t ai, float bd, int32_t bi) {
+    return ad < bd || (ad == bd && ai < bi);
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int32_t lane_read(int32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+// DPP wave_shr:1 — lane l receives lane l-1's value (lane 0 keeps its own). One VALU op, no LDS traffic.
+__device__ __forceinline__ float wave_shr1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x138, 0xf, 0xf, false));
+}
+__device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgcn_update_dpp(v, v, 0x138, 0xf, 0xf, false); }
+
+// One sorted list of up to 64*S (dist, id) pairs spread over a wave: entry p lives in lane p % 64, register
+// p / 64. The admission threshold (entry K-1) is wave-uniform, so the compiler keeps it in SGPRs. Every
+// member must be called by all 64 lanes with wave-uniform arguments (control flow stays uniform).
+template <int S>
+struct WaveList {
+    float d[S];
+    int32_t id[S];
+    float thr_d;
+    int32_t thr_i;
+
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            d[s] = INFINITY;
+            id[s] = kEmptyId;
+        }
+        thr_d = INFINITY;
+        thr_i = kEmptyId;
+    }
+
+    // Inserts the wave-uniform pair (x, xi) at its sorted position; entries behind it move one place back.
+    __device__ __forceinline__ void insert(float x, int32_t xi, int K) {
+        const int lane = __lane_id();
+        int pos = 0;  // number of entries strictly before (x, xi); they form a prefix because the list is sorted
+#pragma unroll
+        for (int s = 0; s < S; ++s) pos += __popcll(__ballot(pair_less(d[s], id[s], x, xi)));
+        float carry_d = 0.f;
+        int32_t carry_i = 0;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int p = s * WAVE + lane;
+            float prev_d = wave_shr1(d[s]);
+            int32_t prev_i = wave_shr1(id[s]);
+            if (s > 0 && lane == 0) {  // lane 0 of a later register takes the last entry of the previous one
+                prev_d = carry_d;
+                prev_i = carry_i;
+            }
+            if (s + 1 < S) {
+                carry_d = lane_read(d[s], WAVE - 1);
+                carry_i = lane_read(id[s], WAVE - 1);
+            }
+            const bool keep = p < pos, here = p == pos;
+            d[s] = keep ? d[s] : (here ? x : prev_d);
+            id[s] = keep ? id[s] : (here ? xi : prev_i);
+        }
+        refresh(K);
+    }
+
+    __device__ __forceinline__ void refresh(int K) {
+        const int t = K - 1;
+        if (S == 1 || t < WAVE) {
+            thr_d = lane_read(d[0], t);
+            thr_i = lane_read(id[0], t);
+        } else {
+            thr_d = lane_read(d[S - 1], t - (S - 1) * WAVE);
+            thr_i = lane_read(id[S - 1], t - (S - 1) * WAVE);
+        }
+    }
+
+    // Each lane offers one candidate; admitted ones are inserted one at a time, lowest lane first. The ballot
+    // uses dist <= threshold as a cheap superset test; the exact (dist, id) test is re-done per candidate
+    // because the threshold falls as candidates go in.
+    __device__ __forceinline__ void offer(float x, int32_t xi, bool valid, int K) {
+        uint64_t mask = __ballot(valid && x <= thr_d);
+        while (mask) {
+            const int src = __ffsll(static_cast<unsigned long long>(mask)) - 1;
+            mask &= mask - 1;
+            const float vx = lane_read(x, src);
+            const int32_t vi = lane_read(xi, src);
+            if (pair_less(vx, vi, thr_d, thr_i)) insert(vx, vi, K);
+        }
+    }
+
+    // Writes entries 0..K-1 to dst (LDS or global).
+    __device__ __forceinline__ void store(Pair* dst, int K) const {
+        const int lane = __lane_id();
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int p = s * WAVE + lane;
+            if (p < K) dst[p] = Pair{d[s], id[s]};
+        }
+    }
+};
+
+// Number of entries of the sorted list l[0..K) that precede e: strictly less when strict, else less-or-equal.
+__device__ __forceinline__ int count_before(const Pair* l, int K, Pair e, bool strict) {
+    int lo = 0, hi = K;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const Pair v = l[mid];
+        const bool before = strict ? pair_less(v.d, v.i, e.d, e.i) : !pair_less(e.d, e.i, v.d, v.i);
+        if (before) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Merges L sorted lists of K pairs (lists[l * K + j], in LDS) into their K smallest, written to out[0..K).
+// Rank of an entry = its index in its own list + entries of earlier lists that are <= it + entries of later
+// lists that are < it; ranks are unique even with equal (sentinel) entries. All threads of the block call it;
+// the caller synchronises before (lists written) and after (out read).
+__device__ __forceinline__ void merge_lists(const Pair* lists, int L, int K, Pair* out, int tid, int nthreads) {
+    for (int t = tid; t < L * K; t += nthreads) {
+        const int l = t / K, j = t % K;
+        const Pair e = lists[t];
+        int rank = j;
+        for (int o = 0; o < L && rank < K; ++o)
+            if (o != l) rank += count_before(lists + o * K, K, e, o > l);
+        if (rank < K) out[rank] = e;
+    }
+}
+
+}  // namespace vk

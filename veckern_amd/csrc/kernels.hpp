@@ -1,0 +1,71 @@
+// Internal launch interface between the C-ABI host layer (capi.hip) and the kernel translation units.
+// Nothing here is exported from the shared library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device.hpp"
+
+namespace vk {
+
+// ---- LUT build (lut.hip). Writes lut[g][s][c][qg] for groups g of qg consecutive queries; query slots past nq
+// are written as 0.f so that padded groups hold defined values. groups >= ceil(nq / qg).
+hipError_t launch_lut(const float* queries, const float* centroids, int d, int m, int nq, int qg, int groups,
+                      float* lut, hipStream_t stream);
+
+// ---- code layouts (layout.hip). n_pad is a multiple of 64; vectors past n are zero codes.
+// Word-interleaved: out[(tile * (m/16) + w) * 64 + lane] = 16 sub-codes 16w..16w+15 of vector tile*64+lane.
+hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint4* out, hipStream_t stream);
+// Byte-interleaved: out[(tile * m + s) * 64 + lane] = sub-code s of vector tile*64+lane.
+hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint8_t* out,
+                              hipStream_t stream);
+
+// ---- fused scan with wave-cooperative lists (fused_wave_*.hip)
+struct WaveScanArgs {
+    const float* lut;     // [slabs * ng][m][256][qg]
+    const uint4* codes;   // word-interleaved, padded to a multiple of 256 vectors
+    int64_t n;
+    int m;
+    int nq;
+    int K;                // list length, <= 64 * S
+    int64_t n_gran;       // granules (64 * ilp vectors) per slab
+    int64_t total;        // slabs * n_gran
+    int max_slots;        // partial lists per slab, upper bound over slabs
+    Pair* part;           // [slabs][max_slots][qg * ng][K]
+};
+
+struct WaveScanKernel {
+    const void* fn = nullptr;  // kernel symbol, for occupancy queries
+    int threads = 0;
+    bool dynamic_lds = false;  // tables in dynamic LDS (m not fixed at compile time) rather than a static array
+    hipError_t (*launch)(const WaveScanArgs&, int grid, size_t smem, hipStream_t) = nullptr;
+};
+
+// Returns a kernel with fn == nullptr when the combination is not built.
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments);
+
+// Blocks covering slab `slab` in the balanced partition of `total` work items over `grid` blocks
+// (block b owns items [b*total/grid, (b+1)*total/grid)).
+__host__ __device__ inline int64_t first_block_of(int64_t item, int64_t grid, int64_t total) {
+    return ((item + 1) * grid - 1) / total;
+}
+
+// ---- selection / final merge (select.hip)
+struct SelectArgs {
+    int mode;              // 0: rows of distances, ids = column index; 1: grid partials; 2: balanced-partition partials
+    const float* dists;    // mode 0: [nq][len]
+    int64_t len;
+    const Pair* part;      // modes 1, 2
+    int K;                 // list length of the selection (and of each partial list)
+    int64_t bx;            // mode 1: partial lists per query, layout [q][bx][K]
+    int qs;                // mode 2: queries per slab
+    int max_slots;         // mode 2
+    int64_t n_gran, total, grid;  // mode 2 partition
+    int k;                 // results written per query
+    Pair* out;             // [nq][k]; empty slots become {+inf, -1}
+};
+hipError_t launch_select(const SelectArgs& a, int nq, hipStream_t stream);
+
+}  // namespace vk

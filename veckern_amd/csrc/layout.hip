@@ -1,0 +1,50 @@
+// One-time code layout transforms, run on the GPU when a variant first needs them (reference:
+// build_interleaved_bytes / build_interleaved_words, searcher.cu:103-119, formulas kernels.cuh:92-94, 238-240).
+// Tiles are 64 vectors (one wave64) instead of the reference's 32. Every output element is written once, with
+// coalesced stores; the strided row-major reads are a one-off cost.
+#include "kernels.hpp"
+
+namespace vk {
+
+__global__ void __launch_bounds__(256)
+    build_words_kernel(const uint8_t* __restrict__ codes, int64_t n, int words, int64_t total, uint4* __restrict__ out) {
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total;
+         o += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t lane = o % WAVE, w = (o / WAVE) % words, tile = o / (static_cast<int64_t>(WAVE) * words);
+        const int64_t i = tile * WAVE + lane;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (i < n) v = *reinterpret_cast<const uint4*>(codes + (i * words + w) * 16);
+        out[o] = v;
+    }
+}
+
+__global__ void __launch_bounds__(256)
+    build_bytes_kernel(const uint8_t* __restrict__ codes, int64_t n, int m, int64_t total, uint8_t* __restrict__ out) {
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total;
+         o += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t lane = o % WAVE, s = (o / WAVE) % m, tile = o / (static_cast<int64_t>(WAVE) * m);
+        const int64_t i = tile * WAVE + lane;
+        out[o] = i < n ? codes[i * m + s] : 0;
+    }
+}
+
+static int layout_grid(int64_t total) {
+    const int64_t blocks = (total + 255) / 256;
+    return static_cast<int>(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
+}
+
+hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint4* out, hipStream_t stream) {
+    const int words = m / 16;
+    const int64_t total = n_pad * words;  // uint4 elements
+    hipLaunchKernelGGL(build_words_kernel, dim3(layout_grid(total)), dim3(256), 0, stream, codes, n, words, total, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint8_t* out,
+                              hipStream_t stream) {
+    const int64_t total = n_pad * m;
+    hipLaunchKernelGGL(build_bytes_kernel, dim3(layout_grid(total)), dim3(256), 0, stream, codes, n, m, total, out);
+    return hipGetLastError();
+}
+
+}  // namespace vk

@@ -1,0 +1,63 @@
+// Host-side launch planning shared by the C ABI and its CPU tests: list-length dispatch, queries-per-block
+// capping, the balanced work partition of the wave-list scan, and the blocks_x model of the grid kernels.
+#pragma once
+
+#include <algorithm>
+#include <cstddef>
+#include <cstdint>
+
+namespace vk::plan {
+
+// Smallest supported list length >= k (searcher.cu:86-90); 0 when k > 128.
+inline int dispatched_k(size_t k) {
+    for (int K : {8, 16, 32, 64, 128})
+        if (k <= static_cast<size_t>(K)) return K;
+    return 0;
+}
+
+// v3-v5 read the byte-interleaved layout, v6-v8 the 16-byte-word one (searcher.cu:222-241).
+inline bool uses_byte_layout(int v) { return v == 3 || v == 4 || v == 5; }
+inline bool uses_word_layout(int v) { return v == 6 || v == 7 || v == 8; }
+
+// Queries per block: the requested Q, halved until the Q tables (Q * m KB) fit in LDS; for per-thread lists
+// (v7) also until Q * K <= 64, as searcher.cu:213-220.
+inline int effective_q(int requested, size_t m, size_t max_lds, bool per_thread_lists, int K) {
+    int q = std::max(requested, 1);
+    while (q > 1 && ((per_thread_lists && q * K > 64) || static_cast<size_t>(q) * m * 256 * sizeof(float) > max_lds))
+        q /= 2;
+    return q;
+}
+
+// First block whose range [b*total/grid, (b+1)*total/grid) contains `item`.
+inline int64_t first_block(int64_t item, int64_t grid, int64_t total) { return ((item + 1) * grid - 1) / total; }
+
+// Balanced partition of the wave-list scan: slabs of q queries, each cut into granules of 64*ilp vectors;
+// the slabs*n_gran items are split evenly over `grid` blocks. grid = resident blocks (slots) unless
+// blocks_per_query asks for a fixed number of blocks per slab.
+struct Partition {
+    int64_t slabs = 0, n_gran = 0, total = 0, grid = 0;
+    int max_slots = 0;  // most blocks touching one slab = partial lists per query
+};
+
+inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_t slots, int blocks_per_query) {
+    Partition p;
+    p.slabs = static_cast<int64_t>((nq + q - 1) / q);
+    const int64_t tiles = (n + 63) / 64;
+    p.n_gran = (tiles + ilp - 1) / ilp;
+    p.total = p.slabs * p.n_gran;
+    if (blocks_per_query > 0)
+        p.grid = p.slabs * std::min<int64_t>(blocks_per_query, p.n_gran);
+    else
+        p.grid = std::min<int64_t>(std::max<int64_t>(slots, 1), p.total);
+    // Keep grid * total (the kernel's range arithmetic) and the grid size itself in range.
+    const int64_t limit = std::min<int64_t>(int64_t{1} << 31 >> 1, (int64_t{1} << 62) / std::max<int64_t>(p.total, 1));
+    p.grid = std::max<int64_t>(1, std::min(p.grid, limit));
+    for (int64_t slab = 0; slab < p.slabs; ++slab) {
+        const int64_t lo = first_block(slab * p.n_gran, p.grid, p.total);
+        const int64_t hi = first_block((slab + 1) * p.n_gran - 1, p.grid, p.total);
+        p.max_slots = std::max<int>(p.max_slots, static_cast<int>(hi - lo + 1));
+    }
+    return p;
+}
+
+}  // namespace vk::plan

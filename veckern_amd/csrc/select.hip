@@ -1,0 +1,74 @@
+// Top-k selection (reference: select_kernel, kernels.cuh:179-202, launched by searcher.cu:285-296).
+// One block per query. Each wave streams its share of the candidates into a wave-cooperative sorted list
+// (threshold test per candidate, rare inserts), then the four wave lists are merged by rank. Three candidate
+// sources share the kernel:
+//   mode 0 — a row of n distances, ids are column indices (unfused scans);
+//   mode 1 — bx partial K-lists per query laid out [q][bx][K] (per-thread-list fused scans);
+//   mode 2 — partial K-lists of the balanced partition of the wave-list scan, [slab][slot][query][K].
+// Empty slots ({+inf, INT32_MAX}) are skipped, like the reference skips id < 0, and the output turns any that
+// remain into {+inf, -1}.
+#include "kernels.hpp"
+
+namespace vk {
+
+template <int S>
+__global__ void __launch_bounds__(256) select_kernel(SelectArgs a) {
+    constexpr int T = 256, W = T / WAVE;
+    __shared__ Pair buf[(W + 1) * WAVE * S];
+    const int64_t q = blockIdx.x;
+    const int tid = threadIdx.x, lane = __lane_id(), wave = tid / WAVE;
+    const int K = a.K;
+
+    WaveList<S> list;
+    list.init();
+    if (a.mode == 0) {
+        const float* row = a.dists + q * a.len;
+        for (int64_t base = static_cast<int64_t>(wave) * WAVE; base < a.len; base += W * WAVE) {
+            const int64_t j = base + lane;
+            const bool valid = j < a.len;
+            const float x = valid ? row[j] : INFINITY;
+            list.offer(x, static_cast<int32_t>(j), valid, K);
+        }
+    } else {
+        const Pair* first;
+        int64_t count, stride;
+        if (a.mode == 1) {
+            first = a.part + q * a.bx * K;
+            count = a.bx;
+            stride = K;
+        } else {
+            const int64_t slab = q / a.qs, qq = q % a.qs;
+            const int64_t lo = first_block_of(slab * a.n_gran, a.grid, a.total);
+            const int64_t hi = first_block_of((slab + 1) * a.n_gran - 1, a.grid, a.total);
+            count = hi - lo + 1;
+            first = a.part + (slab * a.max_slots * a.qs + qq) * K;
+            stride = static_cast<int64_t>(a.qs) * K;
+        }
+        const int64_t all = count * K;
+        for (int64_t base = static_cast<int64_t>(wave) * WAVE; base < all; base += W * WAVE) {
+            const int64_t e = base + lane;
+            Pair p{INFINITY, kEmptyId};
+            if (e < all) p = first[(e / K) * stride + e % K];
+            list.offer(p.d, p.i, p.i != kEmptyId, K);
+        }
+    }
+
+    Pair* merged = buf + W * K;
+    list.store(buf + wave * K, K);
+    __syncthreads();
+    merge_lists(buf, W, K, merged, tid, T);
+    __syncthreads();
+    for (int j = tid; j < a.k; j += T) {
+        const Pair p = merged[j];
+        a.out[q * a.k + j] = p.i == kEmptyId ? Pair{INFINITY, -1} : p;
+    }
+}
+
+hipError_t launch_select(const SelectArgs& a, int nq, hipStream_t stream) {
+    if (a.K <= WAVE) hipLaunchKernelGGL(select_kernel<1>, dim3(nq), dim3(256), 0, stream, a);
+    else if (a.K <= 2 * WAVE) hipLaunchKernelGGL(select_kernel<2>, dim3(nq), dim3(256), 0, stream, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace vk
