@@ -1,0 +1,264 @@
+#!/usr/bin/env python3
+"""Benchmark of the PQ search hot path on one MI355X: per-query LUT build, fused ADC scan and top-k.
+
+A step is one search of the whole query batch against the whole database (LUT build + fused scan + final
+merge), with queries and results resident in HBM (the device entry point vk_search_device). The default workload
+is the headline configuration: 1M vectors of d=128 from a 1000-component Gaussian mixture (sigma 0.3), PQ m=16
+trained by 25 k-means iterations on the first 50k vectors, nq=1000 queries from the same mixture, k=10, fp32 LUTs.
+
+Prints ONE JSON line on stdout (progress goes to stderr):
+  value        queries/s over the timed steps (wall clock, device synchronised on both sides)
+  roofline     the fused scan kernel against the measured LDS random-lookup floor (HIP events on its stream),
+               plus its algorithmic HBM bytes against the 8 TB/s peak
+  cpu_baseline the reference's CPU adc_search (compiled from its sources into oracle/_ref) or, if that library is
+               absent, the oracle port, on a bounded sample of the same queries on this host's cores
+  parity       the GPU results for the CPU sample compared with the CPU results (ids and distance bits)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config B|A|C32|C64|D|D1|E] [--queries-per-block Q]
+                       [--ilp U] [--variant v8] [--no-cpu] [--no-recall]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "queries/s @1M vecs m=16 k=10 nq=1000; % of LDS-lookup/HBM roofline"
+A100_V8_QPS = 86216.0  # reference v8 at 1M x d128, PQ16, nq=1000, k=10 (results/final/scaling.csv:11)
+HBM_PEAK_GBS = 8000.0   # MI355X published HBM3E bandwidth
+
+# name -> (n, d, m, nq, k, data, train rows, iters, description)
+CONFIGS = {
+    "A": (100_000, 128, 16, 100, 10, "mixture", 50_000, 25, "pq-scan 100k x d128, m16, nq=100, k=10"),
+    "B": (1_000_000, 128, 16, 1000, 10, "mixture", 50_000, 25, "pq-scan 1M x d128, m16 (16 B codes), nq=1000, k=10"),
+    "C32": (1_000_000, 128, 32, 1000, 100, "mixture", 50_000, 25, "pq-scan 1M x d128, m32, nq=1000, k=100"),
+    "C64": (1_000_000, 128, 64, 1000, 100, "mixture", 50_000, 25, "pq-scan 1M x d128, m64, nq=1000, k=100"),
+    "D": (10_000_000, 128, 16, 1000, 10, "mixture", 50_000, 25, "pq-scan 10M x d128, m16, nq=1000, k=10"),
+    "D1": (10_000_000, 128, 16, 1, 10, "mixture", 50_000, 25, "pq-scan 10M x d128, m16, nq=1, k=10 (latency)"),
+    "E": (100_000_000, 128, 16, 1000, 10, "codes", 0, 0, "pq-scan 100M direct uniform codes, m16, nq=1000, k=10"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_workload(cfg):
+    """Seeded synthetic data of the configuration: (centroids, codes, queries, base or None)."""
+    from veckern_amd import host
+    n, d, m, nq, k, data, train, iters, _ = CONFIGS[cfg]
+    t0 = time.time()
+    if data == "mixture":
+        base = host.gaussian_mixture(d, 1000, 0.3, 1, 0, n)
+        queries = host.gaussian_mixture(d, 1000, 0.3, 1, 1 << 40, nq)  # a disjoint row range of the same mixture
+        centroids = host.pq_train(base[:min(train, n)], m, iters, seed=1)
+        codes = host.pq_encode(centroids, base)
+    else:  # codes drawn directly: uniform bytes, N(0, 1) codebooks and queries
+        base = None
+        codes = host.uniform_codes(0, n, m, 1)
+        centroids = host.normal_values(1, host.STREAM_CODEBOOK, 0, m * 256 * (d // m)).reshape(m, 256, d // m)
+        queries = host.normal_values(1, host.STREAM_QUERIES, 0, nq * d).reshape(nq, d)
+    log(f"[bench] workload {cfg}: n={n} d={d} m={m} nq={nq} k={k} built in {time.time() - t0:.1f} s")
+    return centroids, codes, queries, base
+
+
+def microbench():
+    """Measured roofline peaks: LDS random-lookup floor (best table width) and HBM streaming read."""
+    import veckern_amd as vk
+    vk.library()
+    lib = ctypes.CDLL(os.path.join(ROOT, "veckern_amd", "lib", "libveckern_bench.so"))
+    lib.vkb_lds_floor.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_double)]
+    lib.vkb_hbm_read.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    floors = {}
+    for qg in (1, 2, 4):
+        rate, ms = ctypes.c_double(), ctypes.c_double()
+        if lib.vkb_lds_floor(qg, 2000, 3, ctypes.byref(rate), ctypes.byref(ms)) != 0:
+            raise RuntimeError("LDS floor microbenchmark failed")
+        floors[qg] = rate.value
+    gbs = ctypes.c_double()
+    if lib.vkb_hbm_read(1600 << 20, 5, ctypes.byref(gbs)) != 0:
+        raise RuntimeError("HBM read microbenchmark failed")
+    return floors, gbs.value
+
+
+def cpu_baseline(centroids, codes, queries, k, d, target_s=10.0):
+    """Times the CPU search on a bounded sample of the queries; returns (record, results of the sample)."""
+    from oracle import binding as orc
+    nq = queries.shape[0]
+    use_ref = orc.ref_available()
+    if use_ref:
+        rpq = orc.RefPQ(centroids, d)
+        codes_cpu = rpq.remap_codes(codes)
+        run = lambda q: rpq.adc_search(codes_cpu, q, k)
+    else:
+        run = lambda q: orc.adc_search(centroids, d, codes, q, k)
+    cores = orc.max_threads()
+    probe = min(nq, max(1, cores))
+    t0 = time.perf_counter()
+    run(queries[:probe])
+    per_query = (time.perf_counter() - t0) / probe
+    sample = int(min(nq, max(probe, round(target_s / max(per_query, 1e-9)))))
+    t0 = time.perf_counter()
+    res = run(queries[:sample])
+    elapsed = time.perf_counter() - t0
+    rec = {
+        "value": sample / elapsed,
+        "unit": "queries/s",
+        "cores": cores,
+        "kind": "reference" if use_ref else "port",
+        "sample": f"first {sample} of the {nq} queries against all {codes.shape[0]} codes, k={k}, "
+                  f"{elapsed:.2f} s wall on {cores} OpenMP threads "
+                  + ("(reference src/cpu/cpu_ref.cpp adc_search, -O3 -fopenmp)" if use_ref
+                     else "(oracle port of cpu_ref.cpp adc_search, -O3 -fopenmp)"),
+    }
+    return rec, res
+
+
+def load_traffic(cfg):
+    """HBM bytes per scan launch measured with rocprofv3 --pmc (profiles/traffic.json), if recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(cfg)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="B", choices=sorted(CONFIGS))
+    ap.add_argument("--variant", default="v8")
+    ap.add_argument("--queries-per-block", type=int, default=4)
+    ap.add_argument("--ilp", type=int, default=4)
+    ap.add_argument("--blocks-per-query", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and its parity check")
+    ap.add_argument("--no-recall", action="store_true", help="skip the exact ground truth and recall")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the search path is built and "
+              f"measured on a single MI355X; multi-GPU sharding is a design note, not a code path)", file=sys.stderr)
+        sys.exit(2)
+
+    import veckern_amd as vk
+    variant = next(v for v in vk.ScanVariant if vk.variant_name(v).startswith(args.variant))
+    n, d, m, nq, k, data, _, _, desc = CONFIGS[args.config]
+    centroids, codes, queries, base = make_workload(args.config)
+
+    floors, hbm_gbs = microbench()
+    best_qg = max(floors, key=floors.get)
+    log(f"[bench] LDS floor: " + ", ".join(f"QG{q} {r / 1e12:.2f} Tlookup/s" for q, r in floors.items())
+        + f"; HBM read {hbm_gbs:.0f} GB/s")
+
+    s = vk.PQSearcher(centroids, codes, d)
+    s.set_tuning(vk.Tuning(queries_per_block=args.queries_per_block, vectors_per_step=args.ilp,
+                           blocks_per_query=args.blocks_per_query))
+    dq = vk.DeviceArray.from_host(queries)
+    dout = vk.DeviceArray(nq * k * 8)
+    for _ in range(args.warmup):
+        s.search_device(dq.address, nq, k, variant, dout.address)
+    shape = s.last_launch()
+
+    totals = vk.Timings()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        t = s.search_device(dq.address, nq, k, variant, dout.address)
+        totals.lut_ms += t.lut_ms
+        totals.scan_ms += t.scan_ms
+        totals.select_ms += t.select_ms
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    qps = nq * args.steps / elapsed
+    scan_ms = totals.scan_ms / args.steps
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {qps:,.0f} queries/s; per step LUT "
+        f"{totals.lut_ms / args.steps:.3f} + scan {scan_ms:.3f} + select {totals.select_ms / args.steps:.3f} ms")
+
+    out = np.empty((nq, k), dtype=vk.NEIGHBOR_DTYPE)
+    dout.download(out)
+
+    # Host-buffer path (queries in and results out over PCIe), reported beside the device-resident value.
+    _, _, th = s.search(queries, k, variant)
+    host_qps = nq / (th.total_ms() * 1e-3)
+
+    lookups = float(n) * m * nq
+    achieved = lookups / (scan_ms * 1e-3)
+    q_eff = shape.queries_per_block
+    hbm_bytes = float(n) * m * math.ceil(nq / q_eff)
+    roofline = {
+        "bound": "lds",
+        "achieved": achieved / 1e12,
+        "peak": floors[best_qg] / 1e12,
+        "unit": "Tlookup/s",
+        "frac": achieved / floors[best_qg],
+        "traffic": load_traffic(args.config),
+        "kernel": "fused_wave_kernel_t (scan + per-wave top-k)",
+        "kernel_ms": scan_ms,
+        "algorithmic": f"n*m*nq = {lookups:.3e} LDS lookups per launch (one 4-byte table read + one fp32 add each)",
+        "floor_by_table_width": {f"b{32 * q}_Q{q}": floors[q] / 1e12 for q in floors},
+        "hbm": {"achieved_gbs": hbm_bytes / (scan_ms * 1e-3) / 1e9, "peak_gbs": HBM_PEAK_GBS,
+                "frac": hbm_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "measured_read_gbs": hbm_gbs,
+                "algorithmic_bytes": hbm_bytes,
+                "note": "n*m code bytes per slab of Q queries, ceil(nq/Q) slabs per launch"},
+    }
+
+    record = {
+        "metric": METRIC,
+        "value": qps,
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": qps / A100_V8_QPS if args.config == "B" else None,
+        "dtype": "f32",
+        "data": ("synthetic: seeded 1000-component Gaussian mixture (sigma 0.3), PQ trained by seeded k-means"
+                 if data == "mixture" else "synthetic: seeded uniform codes, N(0,1) codebooks and queries"),
+        "config": {"workload": desc, "n": n, "d": d, "m": m, "nq": nq, "k": k, "variant": vk.variant_name(variant),
+                   "queries_per_block": shape.queries_per_block, "vectors_per_step": shape.vectors_per_step,
+                   "threads": shape.threads, "blocks": shape.blocks_x, "blocks_per_cu": shape.blocks_per_sm},
+        "roofline": roofline,
+        "stage_ms": {"lut": totals.lut_ms / args.steps, "scan": scan_ms, "select": totals.select_ms / args.steps},
+        "qps_host_buffers": host_qps,
+    }
+
+    if not args.no_recall and base is not None:
+        from veckern_amd import host
+        ev = min(100, nq)
+        gt = host.exact_knn(base, queries[:ev], k)
+        record["recall_at_k"] = host.recall_at_k(out[:ev], gt["id"], k)
+        log(f"[bench] recall@{k} over {ev} queries: {record['recall_at_k']:.4f}")
+
+    if not args.no_cpu:
+        rec, res = cpu_baseline(centroids, codes, queries, k, d)
+        record["cpu_baseline"] = rec
+        sample = res.shape[0]
+        same_ids = bool((res["id"] == out[:sample]["id"]).all())
+        same_bits = bool((res["dist"].view(np.uint32) == out[:sample]["dist"].view(np.uint32)).all())
+        record["parity"] = {"queries": sample, "ids_identical": same_ids, "dist_bits_identical": same_bits,
+                            "against": rec["kind"]}
+        log(f"[bench] CPU {rec['kind']}: {rec['value']:.1f} queries/s on {rec['cores']} threads; parity ids "
+            f"{same_ids} dist bits {same_bits}")
+    else:
+        record["cpu_baseline"] = None
+
+    s.close()
+    print(json.dumps(record), flush=True)
+
+
+if __name__ == "__main__":
+    main()

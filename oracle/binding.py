@@ -128,3 +128,76 @@ def topk_run(dists, ids, k: int, use_ref: bool = False) -> np.ndarray:
     fn = ref().vkref_topk_run if use_ref else oracle().vko_topk_run
     fn(d.ctypes.data, i.ctypes.data, d.size, k, out.ctypes.data)
     return out
+
+
+# ---------------------------------------------------------------- the reference's own CPU library (oracle/_ref)
+
+class RefPQ:
+    """A reference ProductQuantizer (oracle/_ref) holding a given codebook.
+
+    The reference class has no codebook setter, so it is trained for 0 iterations on 256 points whose s-th
+    sub-vectors are the 256 given centroids of sub-space s: its initialisation then copies exactly those points,
+    in a shuffled order per sub-space (pq.cpp:41-45). `perm[s][c]` is the given centroid the reference stores at
+    index c; `remap_codes` translates codes written against the given codebook into the reference's indices.
+    """
+
+    def __init__(self, centroids: np.ndarray, d: int):
+        cent = _c(centroids, np.float32)
+        m = cent.shape[0]
+        dsub = d // m
+        cent = cent.reshape(m, 256, dsub)
+        points = np.ascontiguousarray(cent.transpose(1, 0, 2).reshape(256, d))
+        lib = ref()
+        self._h = lib.vkref_pq_create(d, m)
+        if not self._h:
+            raise ValueError("reference ProductQuantizer rejected (d, m)")
+        if lib.vkref_pq_train(self._h, points.ctypes.data, 256, 0, 1) != 0:
+            raise ValueError("reference training failed")
+        got = np.empty((m, 256, dsub), dtype=np.float32)
+        lib.vkref_pq_centroids(self._h, got.ctypes.data)
+        self.d, self.m = d, m
+        self.perm = np.empty((m, 256), dtype=np.int64)
+        self.inverse = np.empty((m, 256), dtype=np.uint8)
+        for s in range(m):
+            # match each stored centroid to a given one (identical rows: any of them gives identical distances)
+            keys = {cent[s, c].tobytes(): c for c in range(255, -1, -1)}
+            self.perm[s] = [keys[got[s, c].tobytes()] for c in range(256)]
+            self.inverse[s, self.perm[s]] = np.arange(256, dtype=np.uint8)
+        self.centroids = got
+
+    def remap_codes(self, codes: np.ndarray) -> np.ndarray:
+        codes = _c(codes, np.uint8)
+        out = np.empty_like(codes)
+        for s in range(self.m):
+            out[:, s] = self.inverse[s][codes[:, s]]
+        return out
+
+    def adc_search(self, codes_ref: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
+        """The reference's adc_search (cpu_ref.cpp:38-54); codes must already be remapped."""
+        codes_ref = _c(codes_ref, np.uint8)
+        q = _c(queries, np.float32).reshape(-1, self.d)
+        out = np.empty((q.shape[0], k), dtype=NEIGHBOR)
+        ref().vkref_adc_search(self._h, codes_ref.ctypes.data, codes_ref.shape[0], q.ctypes.data, q.shape[0], k,
+                               out.ctypes.data)
+        return out
+
+    def compute_lut(self, queries: np.ndarray) -> np.ndarray:
+        q = _c(queries, np.float32).reshape(-1, self.d)
+        lut = np.empty((q.shape[0], self.m, 256), dtype=np.float32)
+        ref().vkref_compute_lut(self._h, q.ctypes.data, q.shape[0], lut.ctypes.data)
+        return lut
+
+    def close(self):
+        if self._h:
+            ref().vkref_pq_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def max_threads() -> int:
+    return oracle().vko_max_threads()

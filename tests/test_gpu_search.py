@@ -10,7 +10,7 @@ import pytest
 
 import veckern_amd as vk
 from tests import datagen
-from tests import oracle_binding as orc
+from oracle import binding as orc
 
 pytestmark = pytest.mark.gpu
 

@@ -1,0 +1,149 @@
+"""Host-side tools of veckern_amd (lib/libveckern_cpu.so, include/veckern/host.h): seeded synthetic data, the PQ
+codec and recall evaluation. They build the GPU search's inputs and score its outputs; they are not a search path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import NEIGHBOR_DTYPE, _HERE
+
+LIB_PATH = os.path.join(_HERE, "lib", "libveckern_cpu.so")
+_P, _S = ctypes.c_void_p, ctypes.c_size_t
+_lib = None
+
+# Stream numbers of the N(0, 1) value streams used for directly generated inputs (distinct from the streams the
+# C++ generators use internally).
+STREAM_CODEBOOK = 30
+STREAM_QUERIES = 31
+
+
+def library() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built: run `make -C veckern_amd cpu`")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.vkh_last_error.restype = ctypes.c_char_p
+        lib.vkh_max_threads.restype = ctypes.c_int
+        lib.vkh_philox4x32_10.argtypes = [_P, _P, _P]
+        lib.vkh_philox4x32_10.restype = None
+        lib.vkh_gaussian_mixture.argtypes = [_S, _S, ctypes.c_float, ctypes.c_uint64, _S, _S, _P]
+        lib.vkh_synthetic_source.argtypes = [_S, _S, ctypes.c_uint64, _S, _S, _S, _P]
+        lib.vkh_synthetic_clustered.argtypes = [_S, _S, _S, ctypes.c_uint64, _P]
+        lib.vkh_uniform_codes.argtypes = [_S, _S, _S, ctypes.c_uint64, _P]
+        lib.vkh_normal_values.argtypes = [ctypes.c_uint64, ctypes.c_uint32, _S, _S, _P]
+        lib.vkh_pq_train.argtypes = [_P, _S, _S, _S, _S, ctypes.c_uint64, _P]
+        lib.vkh_pq_encode.argtypes = [_P, _S, _S, _P, _S, _P]
+        lib.vkh_pq_decode.argtypes = [_P, _S, _S, _P, _S, _P]
+        lib.vkh_exact_knn.argtypes = [_P, _S, _P, _S, _S, _S, _P]
+        lib.vkh_rerank_exact.argtypes = [_P, _S, _P, _S, _P, _S, _S, _P]
+        lib.vkh_recall_at_k.restype = ctypes.c_double
+        lib.vkh_recall_at_k.argtypes = [_P, _S, _P, _S, _S, _S]
+        _lib = lib
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(library().vkh_last_error().decode())
+
+
+def max_threads() -> int:
+    return library().vkh_max_threads()
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, dtype=np.uint32)
+    library().vkh_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+    return out
+
+
+def gaussian_mixture(d: int, components: int, sigma: float, seed: int, first: int, count: int) -> np.ndarray:
+    out = np.empty((count, d), dtype=np.float32)
+    _check(library().vkh_gaussian_mixture(d, components, sigma, seed, first, count, out.ctypes.data))
+    return out
+
+
+def synthetic_source(d: int, clusters: int, seed: int, latent_dim: int, first: int, count: int) -> np.ndarray:
+    out = np.empty((count, d), dtype=np.float32)
+    _check(library().vkh_synthetic_source(d, clusters, seed, latent_dim, first, count, out.ctypes.data))
+    return out
+
+
+def synthetic_clustered(n: int, d: int, clusters: int, seed: int) -> np.ndarray:
+    out = np.empty((n, d), dtype=np.float32)
+    _check(library().vkh_synthetic_clustered(n, d, clusters, seed, out.ctypes.data))
+    return out
+
+
+def uniform_codes(first: int, n: int, m: int, seed: int) -> np.ndarray:
+    out = np.empty((n, m), dtype=np.uint8)
+    _check(library().vkh_uniform_codes(first, n, m, seed, out.ctypes.data))
+    return out
+
+
+def normal_values(seed: int, stream: int, first: int, count: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.float32)
+    _check(library().vkh_normal_values(seed, stream, first, count, out.ctypes.data))
+    return out
+
+
+def pq_train(x: np.ndarray, m: int, iters: int, seed: int = 1) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    cent = np.empty((m, 256, d // m), dtype=np.float32)
+    _check(library().vkh_pq_train(x.ctypes.data, n, d, m, iters, seed, cent.ctypes.data))
+    return cent
+
+
+def pq_encode(centroids: np.ndarray, x: np.ndarray) -> np.ndarray:
+    cent = np.ascontiguousarray(centroids, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    m = cent.shape[0]
+    codes = np.empty((n, m), dtype=np.uint8)
+    _check(library().vkh_pq_encode(cent.ctypes.data, d, m, x.ctypes.data, n, codes.ctypes.data))
+    return codes
+
+
+def pq_decode(centroids: np.ndarray, codes: np.ndarray, d: int) -> np.ndarray:
+    cent = np.ascontiguousarray(centroids, dtype=np.float32)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    n, m = codes.shape
+    x = np.empty((n, d), dtype=np.float32)
+    _check(library().vkh_pq_decode(cent.ctypes.data, d, m, codes.ctypes.data, n, x.ctypes.data))
+    return x
+
+
+def exact_knn(base: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
+    base = np.ascontiguousarray(base, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    out = np.empty((q.shape[0], k), dtype=NEIGHBOR_DTYPE)
+    _check(library().vkh_exact_knn(base.ctypes.data, base.shape[0], q.ctypes.data, q.shape[0], base.shape[1], k,
+                                   out.ctypes.data))
+    return out
+
+
+def rerank_exact(base: np.ndarray, queries: np.ndarray, candidates: np.ndarray, k: int) -> np.ndarray:
+    base = np.ascontiguousarray(base, dtype=np.float32)
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    cand = np.ascontiguousarray(candidates, dtype=NEIGHBOR_DTYPE)
+    out = np.empty((q.shape[0], k), dtype=NEIGHBOR_DTYPE)
+    _check(library().vkh_rerank_exact(base.ctypes.data, base.shape[1], q.ctypes.data, q.shape[0], cand.ctypes.data,
+                                      cand.shape[1], k, out.ctypes.data))
+    return out
+
+
+def recall_at_k(found: np.ndarray, truth_ids: np.ndarray, k: int) -> float:
+    """found: (nq, >=k) neighbours; truth_ids: (nq, >=k) int32."""
+    f = np.ascontiguousarray(found, dtype=NEIGHBOR_DTYPE)
+    t = np.ascontiguousarray(truth_ids, dtype=np.int32)
+    r = library().vkh_recall_at_k(f.ctypes.data, f.shape[1], t.ctypes.data, t.shape[1], f.shape[0], k)
+    if r < 0:
+        raise RuntimeError(library().vkh_last_error().decode())
+    return r
