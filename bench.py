@@ -146,7 +146,20 @@ def main():
     ap.add_argument("--blocks-per-query", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and its parity check")
     ap.add_argument("--no-recall", action="store_true", help="skip the exact ground truth and recall")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run one plain device copy of BYTES (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+
+    if args.calibrate_copy:
+        import veckern_amd as vk
+        vk.library()
+        lib = ctypes.CDLL(os.path.join(ROOT, "veckern_amd", "lib", "libveckern_bench.so"))
+        lib.vkb_copy.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+        gbs = ctypes.c_double()
+        if lib.vkb_copy(args.calibrate_copy, 1, ctypes.byref(gbs)) != 0:
+            raise RuntimeError("copy kernel failed")
+        print(json.dumps({"copy_bytes": args.calibrate_copy, "dispatches": 2, "gbs": gbs.value}), flush=True)
+        return
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the search path is built and "
@@ -203,7 +216,8 @@ def main():
         "peak": floors[best_qg] / 1e12,
         "unit": "Tlookup/s",
         "frac": achieved / floors[best_qg],
-        "traffic": load_traffic(args.config),
+        "traffic": (load_traffic(args.config) or {}).get("bytes_per_launch"),
+        "traffic_detail": load_traffic(args.config),
         "kernel": "fused_wave_kernel_t (scan + per-wave top-k)",
         "kernel_ms": scan_ms,
         "algorithmic": f"n*m*nq = {lookups:.3e} LDS lookups per launch (one 4-byte table read + one fp32 add each)",
