@@ -282,21 +282,147 @@ struct vk_searcher {
         clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
     }
 
+    // v0-v3: LUT ([q][s][c]) then the distance matrix of this batch into `dists`.
+    void run_scan(int v, const float* d_q, size_t b, vk_timings* t, StageClock& clock) {
+        const int threads = tuning.scan_threads;
+        const int64_t bx = vk::plan::blocks_x_fill(static_cast<int64_t>(n), static_cast<int64_t>(b), threads,
+                                                   info.sm_count, tuning.blocks_per_query);
+        last = vk_launch_shape{threads, static_cast<int>(bx), static_cast<int>(b), 1, 1, 0, 0.0};
+        lut.ensure(b * m * vk::KSUB);
+        dists.ensure(b * n);
+        clock.time(&t->lut_ms, [&] {
+            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(b), 1,
+                                  static_cast<int>(b), lut.get(), stream));
+        });
+        vk::ScanArgs a{lut.get(), codes.get(), codes_il.get(), static_cast<int64_t>(n), static_cast<int>(m),
+                       dists.get()};
+        clock.time(&t->scan_ms, [&] {
+            VK_HIP(vk::launch_scan(v, a, static_cast<int>(bx), static_cast<int>(b), threads, stream));
+        });
+    }
+
+    void run_unfused(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
+        run_scan(v, d_q, b, t, clock);
+        vk::SelectArgs s{};
+        s.mode = 0;
+        s.dists = dists.get();
+        s.len = static_cast<int64_t>(n);
+        s.K = vk::plan::dispatched_k(kk);
+        s.k = static_cast<int>(kk);
+        s.out = d_out;
+        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
+    }
+
+    // v4-v7: per-thread-list fused scans on a (blocks_x, query groups) grid, then the final merge.
+    void run_thread(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
+        if (v == VK_V4_FUSED)
+            fail(VK_ERR_LOGIC,
+                 "v4_fused is not launched in this build: its run-time-indexed per-thread list faulted the GPU "
+                 "(memory-aperture violation, cause not yet established); use v5_fused_reg or later");
+        const int K = vk::plan::dispatched_k(kk);
+        const int q = v == VK_V7_FUSED_VEC_MQ
+                          ? vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, true, K)
+                          : 1;
+        const int ilp = (v == VK_V6_FUSED_VEC || v == VK_V7_FUSED_VEC_MQ) ? tuning.vectors_per_step : 1;
+        const vk::ThreadScanKernel kern = vk::fused_thread_kernel(v, K, q, ilp);
+        if (!kern.fn) fail(VK_ERR_LOGIC, "no per-thread-list kernel built for this (K, Q, ILP)");
+        const int W = kern.threads / vk::WAVE;
+        const size_t smem = std::max(static_cast<size_t>(q) * m * vk::KSUB * sizeof(float),
+                                     static_cast<size_t>(W + 1) * K * sizeof(Pair));
+        require(smem <= info.max_smem_per_block, "LUT does not fit in LDS");
+        VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+        const int64_t grid_y = (static_cast<int64_t>(b) + q - 1) / q;
+        int64_t bx = 1;
+        last = vk_launch_shape{};
+        if (v == VK_V4_FUSED) {
+            bx = vk::plan::blocks_x_fill(static_cast<int64_t>(n), static_cast<int64_t>(b), 256, info.sm_count,
+                                         tuning.blocks_per_query);
+        } else {
+            int per_cu = 0;
+            VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
+            const vk::plan::WaveChoice c = vk::plan::blocks_x_waves(
+                static_cast<int64_t>(n), grid_y, kern.threads, static_cast<int64_t>(std::max(per_cu, 1)) * info.sm_count,
+                tuning.blocks_per_query);
+            bx = c.blocks_x;
+            last.blocks_per_sm = per_cu;
+            last.waves = c.waves;
+        }
+        bx = std::max<int64_t>(1, std::min<int64_t>(bx, (static_cast<int64_t>(n) + kern.threads - 1) / kern.threads));
+        last.threads = kern.threads;
+        last.blocks_x = static_cast<int>(bx);
+        last.grid_y = static_cast<int>(grid_y);
+        last.queries_per_block = q;
+        last.vectors_per_step = ilp;
+
+        const size_t b_pad = static_cast<size_t>(grid_y) * q;  // tables are read in groups of q
+        lut.ensure(b_pad * m * vk::KSUB);
+        part.ensure(b * static_cast<size_t>(bx) * K);
+        clock.time(&t->lut_ms, [&] {
+            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(b), 1,
+                                  static_cast<int>(b_pad), lut.get(), stream));
+        });
+        vk::ThreadScanArgs a{lut.get(), codes_il.get(), codes_v.get(), static_cast<int64_t>(n), static_cast<int>(m),
+                             static_cast<int>(b), part.get()};
+        clock.time(&t->scan_ms, [&] {
+            VK_HIP(kern.launch(a, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(grid_y)), smem, stream));
+        });
+        vk::SelectArgs s{};
+        s.mode = 1;
+        s.part = part.get();
+        s.K = K;
+        s.bx = bx;
+        s.k = static_cast<int>(kk);
+        s.out = d_out;
+        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
+    }
+
     void run_variant(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
         if (v == VK_V8_FUSED_WARP) return run_wave(d_q, b, kk, d_out, t, clock);
-        fail(VK_ERR_LOGIC, std::string(vk_variant_name(v)) + " is not available in this build");
+        if (vk_is_fused(v)) return run_thread(v, d_q, b, kk, d_out, t, clock);
+        run_unfused(v, d_q, b, kk, d_out, t, clock);
     }
 
     void check_search(size_t kk, int v) const {
         require(valid_variant(v), "unknown scan variant " + std::to_string(v));
+        if (v == VK_V4_FUSED)
+            fail(VK_ERR_LOGIC,
+                 "v4_fused is not launched in this build: its run-time-indexed per-thread list faulted the GPU "
+                 "(memory-aperture violation, cause not yet established); use v5_fused_reg or later");
         require(kk >= 1 && kk <= 128 && kk <= n, "k must be in [1, min(128, n)]");
         validate(v);
     }
 
-    // Queries per launch batch: bounded so the LUT buffer stays under 1 GiB.
-    size_t query_batch() const {
+    // Queries per launch batch: the LUT buffer stays under 1 GiB and, for the unfused variants, the distance
+    // matrix under 512 MiB (searcher.cu:24, 476-477); grid y of the grid kernels stays within 65535.
+    size_t query_batch(int v) const {
         const size_t per_query = m * vk::KSUB * sizeof(float);
-        return std::max<size_t>(1, std::min<size_t>(65536, (size_t{1} << 30) / per_query));
+        size_t batch = std::min<size_t>(65535, (size_t{1} << 30) / per_query);
+        if (!vk_is_fused(v)) batch = std::min(batch, (size_t{512} << 20) / (n * sizeof(float)));
+        return std::max<size_t>(1, batch);
+    }
+
+    void distances_host(const float* host_q, size_t nq, int v, float* host_out, vk_timings* t) {
+        require(valid_variant(v), "unknown scan variant " + std::to_string(v));
+        require(!vk_is_fused(v), "fused variants do not materialise distances");
+        validate(v);
+        use_device();
+        ensure_layout(v);
+        StageClock clock(stream);
+        const size_t batch = query_batch(v);
+        for (size_t q0 = 0; q0 < nq; q0 += batch) {
+            const size_t b = std::min(batch, nq - q0);
+            queries.ensure(b * d);
+            clock.time(&t->transfer_ms, [&] {
+                VK_HIP(hipMemcpyAsync(queries.get(), host_q + q0 * d, b * d * sizeof(float), hipMemcpyHostToDevice,
+                                      stream));
+            });
+            run_scan(v, queries.get(), b, t, clock);
+            clock.time(&t->transfer_ms, [&] {
+                VK_HIP(hipMemcpyAsync(host_out + q0 * n, dists.get(), b * n * sizeof(float), hipMemcpyDeviceToHost,
+                                      stream));
+            });
+            clock.settle();
+        }
     }
 
     void search_host(const float* host_q, size_t nq, size_t kk, int v, vk_neighbor* host_out, vk_timings* t) {
@@ -304,7 +430,7 @@ struct vk_searcher {
         use_device();
         ensure_layout(v);
         StageClock clock(stream);
-        const size_t batch = query_batch();
+        const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
             const size_t b = std::min(batch, nq - q0);
             queries.ensure(b * d);
@@ -327,7 +453,7 @@ struct vk_searcher {
         use_device();
         ensure_layout(v);
         StageClock clock(stream);
-        const size_t batch = query_batch();
+        const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
             const size_t b = std::min(batch, nq - q0);
             run_variant(v, d_q + q0 * d, b, kk, reinterpret_cast<Pair*>(d_out + q0 * kk), t, clock);
@@ -481,12 +607,14 @@ VK_EXPORT int vk_distances(vk_searcher* s, const float* queries, size_t nq, int 
                            vk_timings* timings) {
     return guarded([&] {
         require(s != nullptr, "searcher is null");
-        require(valid_variant(variant), "unknown scan variant");
-        require(!vk_is_fused(variant), "fused variants do not materialise distances");
-        fail(VK_ERR_LOGIC, "distances() is not available in this build");
-        (void)queries;
-        (void)nq;
-        (void)out;
-        (void)timings;
+        vk_timings t{};
+        if (nq > 0) {
+            require(queries != nullptr && out != nullptr, "queries and out must not be null");
+            s->distances_host(queries, nq, variant, out, &t);
+        } else {
+            require(valid_variant(variant), "unknown scan variant");
+            require(!vk_is_fused(variant), "fused variants do not materialise distances");
+        }
+        if (timings) *timings = t;
     });
 }

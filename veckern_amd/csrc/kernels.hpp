@@ -52,6 +52,37 @@ __host__ __device__ inline int64_t first_block_of(int64_t item, int64_t grid, in
     return ((item + 1) * grid - 1) / total;
 }
 
+// ---- unfused scans v0-v3 (scan_thread.hip): dists[q][i] for q < nq, grid (blocks_x, nq)
+struct ScanArgs {
+    const float* lut;         // [nq][m][256]
+    const uint8_t* codes;     // row-major n x m (v0-v2)
+    const uint8_t* codes_il;  // byte-interleaved (v3)
+    int64_t n;
+    int m;
+    float* dists;             // [nq][n]
+};
+hipError_t launch_scan(int variant, const ScanArgs& a, int blocks_x, int nq, int threads, hipStream_t stream);
+
+// ---- fused scans with per-thread lists, v4-v7 (scan_thread.hip): grid (blocks_x, ceil(nq / Q)), 256 threads
+struct ThreadScanArgs {
+    const float* lut;         // [nq padded to a multiple of Q][m][256]; padded tables are zero
+    const uint8_t* codes_il;  // v4, v5
+    const uint4* codes_v;     // v6, v7
+    int64_t n;
+    int m;
+    int nq;
+    Pair* part;               // [nq][blocks_x][K]
+};
+
+struct ThreadScanKernel {
+    const void* fn = nullptr;
+    int threads = 0;
+    hipError_t (*launch)(const ThreadScanArgs&, dim3 grid, size_t smem, hipStream_t) = nullptr;
+};
+
+// The instance for a variant (4-7), list length K and the effective Q (v7) and ILP (v6, v7).
+ThreadScanKernel fused_thread_kernel(int variant, int K, int q, int ilp);
+
 // ---- selection / final merge (select.hip)
 struct SelectArgs {
     int mode;              // 0: rows of distances, ids = column index; 1: grid partials; 2: balanced-partition partials

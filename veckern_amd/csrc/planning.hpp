@@ -60,4 +60,44 @@ inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_
     return p;
 }
 
+// blocks_x of the unfused scans and v4 (searcher.cu:172-177): an override, else about 8 blocks per CU over the
+// whole grid, never fewer than 16 vectors per thread.
+inline int64_t blocks_x_fill(int64_t n, int64_t grid_y, int threads, int cus, int blocks_per_query) {
+    if (blocks_per_query > 0) return blocks_per_query;
+    const int64_t by_work = (n + int64_t{threads} * 16 - 1) / (int64_t{threads} * 16);
+    const int64_t to_fill = (int64_t{8} * cus + grid_y - 1) / grid_y;
+    return std::max<int64_t>(1, std::min(by_work, to_fill));
+}
+
+// blocks_x of the per-thread-list fused scans v5-v7 (searcher.cu:184-208): a wave is the number of blocks resident
+// at once (occupancy API); run time is taken as proportional to ceil(bx * grid_y / wave) / bx, and a larger bx is
+// chosen only when it is at least 2% cheaper. bx is capped at max(64, 4 waves' worth per query row) and at 16
+// vectors per thread.
+struct WaveChoice {
+    int64_t blocks_x = 1;
+    double waves = 0.0;
+};
+
+inline WaveChoice blocks_x_waves(int64_t n, int64_t grid_y, int threads, int64_t resident, int blocks_per_query) {
+    const int64_t wave = std::max<int64_t>(resident, 1);
+    WaveChoice c;
+    if (blocks_per_query > 0) {
+        c.blocks_x = blocks_per_query;
+    } else {
+        const int64_t cap = std::max<int64_t>(64, 4 * ((wave + grid_y - 1) / grid_y));
+        const int64_t useful = (n + int64_t{threads} * 16 - 1) / (int64_t{threads} * 16);
+        const int64_t max_bx = std::max<int64_t>(1, std::min(cap, useful));
+        double best = static_cast<double>((grid_y + wave - 1) / wave);
+        for (int64_t bx = 2; bx <= max_bx; ++bx) {
+            const double cost = static_cast<double>((bx * grid_y + wave - 1) / wave) / static_cast<double>(bx);
+            if (cost < 0.98 * best) {
+                best = cost;
+                c.blocks_x = bx;
+            }
+        }
+    }
+    c.waves = static_cast<double>(c.blocks_x * grid_y) / static_cast<double>(wave);
+    return c;
+}
+
 }  // namespace vk::plan
