@@ -159,10 +159,14 @@ class RefPQ:
         self.perm = np.empty((m, 256), dtype=np.int64)
         self.inverse = np.empty((m, 256), dtype=np.uint8)
         for s in range(m):
-            # match each stored centroid to a given one (identical rows: any of them gives identical distances)
-            keys = {cent[s, c].tobytes(): c for c in range(255, -1, -1)}
-            self.perm[s] = [keys[got[s, c].tobytes()] for c in range(256)]
-            self.inverse[s, self.perm[s]] = np.arange(256, dtype=np.uint8)
+            # Match stored and given centroids by value. Equal vectors give equal LUT entries, so with repeated
+            # centroids any index holding the same vector is a valid match, in either direction.
+            given_of, ref_of = {}, {}
+            for c in range(256):
+                given_of.setdefault(cent[s, c].tobytes(), c)
+                ref_of.setdefault(got[s, c].tobytes(), c)
+            self.perm[s] = [given_of[got[s, r].tobytes()] for r in range(256)]
+            self.inverse[s] = [ref_of[cent[s, c].tobytes()] for c in range(256)]
         self.centroids = got
 
     def remap_codes(self, codes: np.ndarray) -> np.ndarray:

@@ -1,0 +1,207 @@
+// The reference's GPU test cases (tests/test_gpu.cpp:62-202) restated against this build's C++ API
+// (veckern::gpu::PQSearcher over the C ABI), with the oracle (oracle/vk_oracle.h) as the expected answer and a
+// bit-exact bar: identical ids and identical distance bits, where the reference allowed 1e-3 and 99% agreement.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "check.hpp"
+#include "veckern/gpu.hpp"
+#include "veckern/io.hpp"
+#include "veckern/pq.hpp"
+#include "vk_oracle.h"
+
+using namespace veckern;
+using gpu::ScanVariant;
+
+namespace {
+
+struct Fixture {
+    // n is not a multiple of 64 or of any block size, so tails and padding are exercised; nq is prime.
+    std::size_t n = 50'003, d = 64, m = 16, nq = 37;
+    std::vector<float> base = synthetic_clustered(n, d, 50, 11);
+    std::vector<float> queries = synthetic_clustered(nq, d, 50, 12);
+    ProductQuantizer pq{d, m};
+    std::vector<uint8_t> codes = std::vector<uint8_t>(n * m);
+    Fixture() {
+        pq.train(base.data(), 20'000, 8);
+        pq.encode(base.data(), n, codes.data());
+    }
+};
+
+Fixture& fixture() {
+    static Fixture f;
+    return f;
+}
+
+std::vector<vko_neighbor> oracle_search(const ProductQuantizer& pq, const std::vector<uint8_t>& codes, std::size_t n,
+                                        const float* queries, std::size_t nq, std::size_t k) {
+    std::vector<vko_neighbor> out(nq * k);
+    if (vko_adc_search(pq.centroids().data(), pq.d(), pq.m(), codes.data(), n, queries, nq, k, out.data()) != 0)
+        throw std::runtime_error("oracle rejected its input");
+    return out;
+}
+
+void same(const std::vector<Neighbor>& got, const std::vector<vko_neighbor>& expected, const char* what) {
+    EXPECT(got.size() == expected.size());
+    for (std::size_t j = 0; j < got.size(); ++j) {
+        uint32_t a, b;
+        std::memcpy(&a, &got[j].dist, 4);
+        std::memcpy(&b, &expected[j].dist, 4);
+        if (got[j].id != expected[j].id || a != b)
+            vktest::fail_at(__FILE__, __LINE__, std::string(what) + ": mismatch at " + std::to_string(j));
+    }
+}
+
+void check_search(std::size_t k, ScanVariant v, const gpu::Tuning& tuning = {}) {
+    auto& f = fixture();
+    const auto expected = oracle_search(f.pq, f.codes, f.n, f.queries.data(), f.nq, k);
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    searcher.set_tuning(tuning);
+    std::vector<Neighbor> got(f.nq * k);
+    searcher.search(f.queries.data(), f.nq, k, v, got.data());
+    same(got, expected, gpu::variant_name(v));
+    for (std::size_t q = 0; q < f.nq; ++q)
+        for (std::size_t j = 1; j < k; ++j) EXPECT(!(got[q * k + j] < got[q * k + j - 1]));
+}
+
+const ScanVariant kScans[] = {ScanVariant::GlobalLut, ScanVariant::SharedLut, ScanVariant::SharedLutVec,
+                              ScanVariant::Interleaved};
+// v4 is rejected before launch in this build (see the case "v4 is rejected").
+const ScanVariant kFused[] = {ScanVariant::FusedReg, ScanVariant::FusedVec, ScanVariant::FusedVecMQ,
+                              ScanVariant::FusedWarp};
+
+}  // namespace
+
+CASE("device info is sane") {
+    const auto info = gpu::device_info();
+    std::printf("      %s, %d CUs, %.0f GB/s peak, %zu B LDS/block\n", info.name.c_str(), info.sm_count,
+                info.peak_bandwidth_gbs, info.max_smem_per_block);
+    EXPECT(info.sm_count > 0 && info.peak_bandwidth_gbs > 0 && info.max_smem_per_block > 0);
+}
+
+CASE("every scan variant reproduces the CPU ADC distances bit for bit") {
+    auto& f = fixture();
+    std::vector<float> lut(f.nq * f.m * 256), expected(f.nq * f.n), got(f.nq * f.n);
+    vko_compute_lut(f.pq.centroids().data(), f.d, f.m, f.queries.data(), f.nq, lut.data());
+    vko_adc_scan(lut.data(), f.nq, f.codes.data(), f.n, f.m, expected.data());
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    for (auto v : kScans) {
+        searcher.distances(f.queries.data(), f.nq, v, got.data());
+        EXPECT(std::memcmp(got.data(), expected.data(), got.size() * sizeof(float)) == 0);
+    }
+}
+
+CASE("search matches the CPU for every variant, k = 10") {
+    for (auto v : kScans) check_search(10, v);
+    for (auto v : kFused) check_search(10, v);
+}
+
+CASE("search covers every K template (k = 1, 16, 33, 100)") {
+    for (std::size_t k : {1, 16, 33, 100}) {
+        check_search(k, ScanVariant::SharedLut);
+        for (auto v : kFused) check_search(k, v);
+    }
+}
+
+CASE("v7 and v8 are exact for every queries-per-block, nq not divisible by Q") {
+    for (int q : {1, 2, 4, 8}) {
+        gpu::Tuning t;
+        t.queries_per_block = q;
+        for (std::size_t k : {1, 8, 10, 32}) check_search(k, ScanVariant::FusedVecMQ, t);
+        for (std::size_t k : {1, 8, 10, 32, 64, 128}) check_search(k, ScanVariant::FusedWarp, t);
+    }
+}
+
+CASE("tuning overrides keep results exact") {
+    for (int threads : {64, 128, 512}) {
+        gpu::Tuning t;
+        t.scan_threads = threads;
+        check_search(10, ScanVariant::SharedLutVec, t);
+    }
+    for (int bpq : {1, 3, 16}) {
+        gpu::Tuning t;
+        t.blocks_per_query = bpq;
+        check_search(10, ScanVariant::FusedReg, t);
+        check_search(10, ScanVariant::FusedVec, t);
+        check_search(10, ScanVariant::FusedVecMQ, t);
+        check_search(10, ScanVariant::FusedWarp, t);
+    }
+    for (int ilp : {2, 4})
+        for (int bpq : {0, 7}) {
+            gpu::Tuning t;
+            t.vectors_per_step = ilp;
+            t.blocks_per_query = bpq;
+            for (std::size_t k : {1, 10, 33}) {
+                check_search(k, ScanVariant::FusedVec, t);
+                check_search(k, ScanVariant::FusedVecMQ, t);
+                check_search(k, ScanVariant::FusedWarp, t);
+            }
+        }
+}
+
+CASE("launch shape is reported and a single query fills the device") {
+    auto& f = fixture();
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    std::vector<Neighbor> out(f.nq * 10);
+    searcher.search(f.queries.data(), f.nq, 10, ScanVariant::FusedVecMQ, out.data());
+    const auto shape = searcher.last_launch();
+    std::printf("      v7: T=%d blocks_x=%d grid_y=%d Q=%d blocks/CU=%d waves=%.2f\n", shape.threads, shape.blocks_x,
+                shape.grid_y, shape.queries_per_block, shape.blocks_per_sm, shape.waves);
+    EXPECT(shape.queries_per_block == 2 && shape.grid_y == 19);  // ceil(37 / 2)
+    EXPECT(shape.blocks_per_sm > 0 && shape.waves > 0);
+
+    std::vector<Neighbor> one(10);
+    searcher.search(f.queries.data(), 1, 10, ScanVariant::FusedWarp, one.data());
+    const auto single = searcher.last_launch();
+    std::printf("      v8, 1 query: blocks=%d waves=%.2f\n", single.blocks_x, single.waves);
+    const double wave = single.blocks_x / single.waves;
+    const double max_useful = std::ceil(static_cast<double>(f.n) / (single.threads * 16.0));
+    EXPECT(single.blocks_x >= std::min(wave, max_useful) - 0.5);
+}
+
+CASE("word-interleaved variants reject m % 16 != 0; v5 accepts it") {
+    auto& f = fixture();
+    ProductQuantizer pq8(f.d, 8);
+    pq8.train(f.base.data(), 5000, 4);
+    std::vector<uint8_t> codes8(f.n * 8);
+    pq8.encode(f.base.data(), f.n, codes8.data());
+    gpu::PQSearcher searcher(pq8, codes8.data(), f.n);
+    std::vector<Neighbor> got(f.nq * 10);
+    for (auto v : {ScanVariant::SharedLutVec, ScanVariant::FusedVec, ScanVariant::FusedVecMQ, ScanVariant::FusedWarp})
+        EXPECT_THROWS(searcher.search(f.queries.data(), f.nq, 10, v, got.data()));
+    searcher.search(f.queries.data(), f.nq, 10, ScanVariant::FusedReg, got.data());
+    same(got, oracle_search(pq8, codes8, f.n, f.queries.data(), f.nq, 10), "v5 m=8");
+}
+
+CASE("v4 is rejected before launch with std::logic_error") {
+    auto& f = fixture();
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    std::vector<Neighbor> out(10);
+    bool logic = false;
+    try {
+        searcher.search(f.queries.data(), 1, 10, ScanVariant::Fused, out.data());
+    } catch (const std::logic_error&) {
+        logic = true;
+    }
+    EXPECT(logic);
+}
+
+CASE("invalid tuning is rejected") {
+    auto& f = fixture();
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    for (auto bad : {gpu::Tuning{100, 0, 2, 1}, gpu::Tuning{256, -1, 2, 1}, gpu::Tuning{256, 0, 3, 1},
+                     gpu::Tuning{256, 0, 2, 3}})
+        EXPECT_THROWS(searcher.set_tuning(bad));
+}
+
+CASE("invalid configurations are rejected") {
+    auto& f = fixture();
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    std::vector<Neighbor> out(129);
+    EXPECT_THROWS(searcher.search(f.queries.data(), 1, 129, ScanVariant::FusedReg, out.data()));
+    EXPECT_THROWS(searcher.search(f.queries.data(), 1, 0, ScanVariant::FusedWarp, out.data()));
+    EXPECT_THROWS(searcher.distances(f.queries.data(), 1, ScanVariant::FusedWarp, nullptr));
+}
+
+int main() { return vktest::run(); }

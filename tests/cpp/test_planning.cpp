@@ -1,0 +1,88 @@
+// Host-side launch planning (veckern_amd/csrc/planning.hpp), on the CPU: list-length dispatch, Q capping, the
+// balanced work partition of the wave-list scan, and the blocks_x models of the grid kernels. The blocks_x model
+// is checked against launch shapes the reference recorded on an A100 (108 SMs, 4 resident blocks per SM).
+#include <cstdint>
+#include <random>
+#include <vector>
+
+#include "check.hpp"
+#include "planning.hpp"
+
+using namespace vk::plan;
+
+CASE("dispatched_k picks the smallest of 8, 16, 32, 64, 128 that holds k") {
+    EXPECT(dispatched_k(1) == 8 && dispatched_k(8) == 8 && dispatched_k(9) == 16 && dispatched_k(10) == 16);
+    EXPECT(dispatched_k(33) == 64 && dispatched_k(64) == 64 && dispatched_k(100) == 128 && dispatched_k(128) == 128);
+    EXPECT(dispatched_k(129) == 0);
+}
+
+CASE("effective_q halves Q until the tables fit and, for per-thread lists, Q*K <= 64") {
+    const std::size_t lds = 160 * 1024;
+    EXPECT(effective_q(4, 16, lds, false, 16) == 4);
+    EXPECT(effective_q(8, 16, lds, false, 16) == 8);   // 128 KB
+    EXPECT(effective_q(8, 32, lds, false, 16) == 4);   // 256 KB -> 128 KB
+    EXPECT(effective_q(4, 64, lds, false, 128) == 2);  // 256 KB -> 128 KB
+    EXPECT(effective_q(8, 16, lds, true, 16) == 4);    // Q*K = 128 -> 64
+    EXPECT(effective_q(2, 16, lds, true, 128) == 1);
+    EXPECT(effective_q(8, 160, lds, false, 8) == 1);
+}
+
+CASE("blocks_x_waves reproduces the reference's recorded launch shapes") {
+    const int64_t wave = 4 * 108;  // A100: 4 resident blocks per SM x 108 SMs
+    // tests/test_gpu.cpp fixture, v7 Q=2 T=128: run_all.log:28 "blocks_x=22 grid_y=19 ... waves=0.97"
+    WaveChoice c = blocks_x_waves(50'003, 19, 128, wave, 0);
+    EXPECT(c.blocks_x == 22);
+    EXPECT(c.waves > 0.96 && c.waves < 0.98);
+    // 1M headline, v8 Q=2 T=256: results/final/scaling.csv:11 "blocks_x 6, grid_y 500"
+    c = blocks_x_waves(1'000'000, 500, 256, wave, 0);
+    EXPECT(c.blocks_x == 6);
+    // 10M, one query, v8 T=256: results/final/latency.csv:17 "bx=430"
+    c = blocks_x_waves(10'000'000, 1, 256, wave, 0);
+    EXPECT(c.blocks_x == 430);
+    // an explicit blocks_per_query wins
+    c = blocks_x_waves(1'000'000, 500, 256, wave, 7);
+    EXPECT(c.blocks_x == 7);
+}
+
+CASE("blocks_x_fill: ~8 blocks per CU over the grid, >= 16 vectors per thread, override wins") {
+    EXPECT(blocks_x_fill(50'003, 37, 256, 256, 0) == 13);      // by work: ceil(50003 / 4096)
+    EXPECT(blocks_x_fill(10'000'000, 1000, 256, 256, 0) == 3);  // to fill: ceil(2048 / 1000)
+    EXPECT(blocks_x_fill(10, 1, 256, 256, 0) == 1);
+    EXPECT(blocks_x_fill(10'000'000, 1000, 256, 256, 5) == 5);
+}
+
+CASE("balanced_partition covers every item exactly once and bounds the slots per slab") {
+    std::mt19937_64 rng(7);
+    for (int trial = 0; trial < 300; ++trial) {
+        const int64_t n = 1 + static_cast<int64_t>(rng() % 200'000);
+        const std::size_t nq = 1 + rng() % 700;
+        const int q = 1 << (rng() % 4);
+        const int ilp = 1 << (rng() % 3);
+        const int64_t slots = 1 + static_cast<int64_t>(rng() % 1100);
+        const int bpq = (trial % 3 == 0) ? static_cast<int>(1 + rng() % 40) : 0;
+        const Partition p = balanced_partition(n, nq, q, ilp, slots, bpq);
+        EXPECT(p.slabs == static_cast<int64_t>((nq + q - 1) / q));
+        EXPECT(p.n_gran == ((n + 63) / 64 + ilp - 1) / ilp);
+        EXPECT(p.total == p.slabs * p.n_gran && p.grid >= 1 && p.grid <= p.total);
+        if (bpq == 0) EXPECT(p.grid <= slots);
+        // block ranges tile [0, total) in order, and every block is non-empty
+        int64_t prev_end = 0;
+        for (int64_t b = 0; b < p.grid; ++b) {
+            const int64_t start = b * p.total / p.grid, end = (b + 1) * p.total / p.grid;
+            EXPECT(start == prev_end && end > start);
+            prev_end = end;
+        }
+        EXPECT(prev_end == p.total);
+        // the blocks touching each slab are [first(slab start), first(slab end - 1)], at most max_slots of them
+        for (int64_t slab = 0; slab < p.slabs; ++slab) {
+            const int64_t lo = first_block(slab * p.n_gran, p.grid, p.total);
+            const int64_t hi = first_block((slab + 1) * p.n_gran - 1, p.grid, p.total);
+            EXPECT(lo * p.total / p.grid <= slab * p.n_gran && slab * p.n_gran < (lo + 1) * p.total / p.grid);
+            EXPECT(hi - lo + 1 <= p.max_slots);
+            if (bpq > 0 && p.grid == p.slabs * std::min<int64_t>(bpq, p.n_gran))
+                EXPECT(hi - lo + 1 == std::min<int64_t>(bpq, p.n_gran));
+        }
+    }
+}
+
+int main() { return vktest::run(); }
