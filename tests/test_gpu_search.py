@@ -63,7 +63,8 @@ def test_fused_warp_every_k(fixture, searcher, k):
     searcher.set_tuning(vk.Tuning())
     d, i, t = searcher.search(queries, k, vk.ScanVariant.FusedWarp)
     assert_same(d, i, expected(fixture, k), f"v8 k={k}")
-    assert t.scan_ms > 0 and t.lut_ms > 0
+    # One launch builds the tables, scans and merges: its whole time is scan_ms.
+    assert t.scan_ms > 0 and t.lut_ms == 0 and t.select_ms == 0
 
 
 @pytest.mark.parametrize("q", [1, 2, 4, 8])
@@ -83,7 +84,7 @@ def test_fused_warp_blocks_per_query(fixture, searcher, bpq):
     _, _, queries = fixture
     for q in (2, 4):
         searcher.set_tuning(vk.Tuning(blocks_per_query=bpq, queries_per_block=q))
-        for k in (1, 10, 33):
+        for k in (1, 10, 33, 128):
             d, i, _ = searcher.search(queries, k, vk.ScanVariant.FusedWarp)
             assert_same(d, i, expected(fixture, k), f"v8 bpq={bpq} Q={q} k={k}")
 

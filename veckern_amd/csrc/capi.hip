@@ -189,6 +189,9 @@ struct vk_searcher {
     DeviceBuffer<uint8_t> codes, codes_il;
     DeviceBuffer<uint4> codes_v;
     DeviceBuffer<Pair> part, out;
+    DeviceBuffer<unsigned> counters;
+    size_t counters_zeroed = 0;
+    bool counters_dirty = false;
     bool have_il = false, have_v = false;
 
     ~vk_searcher() {
@@ -238,9 +241,11 @@ struct vk_searcher {
 
         const vk::plan::Partition part_plan = vk::plan::balanced_partition(
             static_cast<int64_t>(n), b, q, ilp, static_cast<int64_t>(per_cu) * info.sm_count, tuning.blocks_per_query);
-        const size_t groups = static_cast<size_t>(part_plan.slabs) * ng;
-        lut.ensure(groups * qg * m * vk::KSUB);
-        part.ensure(static_cast<size_t>(part_plan.slabs) * part_plan.max_slots * q * K);
+        // Up to 8 blocks per slab every wave leaves its own partial lists; beyond that the block merges its wave
+        // lists first, which keeps the final merge of a slab to at most max(64, blocks per slab) lists per query.
+        const int lists_per_block = part_plan.max_slots > 8 ? 1 : kern.threads / vk::WAVE;
+        part.ensure(static_cast<size_t>(part_plan.slabs) * q * part_plan.max_slots * lists_per_block * K);
+        ensure_counters(static_cast<size_t>(part_plan.slabs));
 
         last = vk_launch_shape{};
         last.threads = kern.threads;
@@ -251,35 +256,38 @@ struct vk_searcher {
         last.blocks_per_sm = per_cu;
         last.waves = static_cast<double>(part_plan.grid) / (static_cast<double>(per_cu) * info.sm_count);
 
-        clock.time(&t->lut_ms, [&] {
-            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(b),
-                                  qg, static_cast<int>(groups), lut.get(), stream));
-        });
+        // One launch: every block builds its slab's tables in LDS, scans, and the last block of each slab merges
+        // the slab's partial lists into d_out. The LUT and the final merge are inside scan_ms.
         vk::WaveScanArgs a{};
-        a.lut = lut.get();
+        a.queries = d_q;
+        a.centroids = centroids.get();
         a.codes = codes_v.get();
         a.n = static_cast<int64_t>(n);
+        a.d = static_cast<int>(d);
         a.m = static_cast<int>(m);
         a.nq = static_cast<int>(b);
         a.K = K;
+        a.k = static_cast<int>(kk);
         a.n_gran = part_plan.n_gran;
         a.total = part_plan.total;
         a.max_slots = part_plan.max_slots;
+        a.lists_per_block = lists_per_block;
         a.part = part.get();
+        a.counters = counters.get();
+        a.out = d_out;
+        counters_dirty = true;  // cleared once the stream completes the launch without error
         clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(part_plan.grid), smem, stream)); });
+    }
 
-        vk::SelectArgs s{};
-        s.mode = 2;
-        s.part = part.get();
-        s.K = K;
-        s.qs = q;
-        s.max_slots = part_plan.max_slots;
-        s.n_gran = part_plan.n_gran;
-        s.total = part_plan.total;
-        s.grid = part_plan.grid;
-        s.k = static_cast<int>(kk);
-        s.out = d_out;
-        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
+    // Per-slab completion counters of the wave-list scan. The kernel leaves them at zero; they are zeroed here
+    // when allocated or grown, and again if a previous launch may have stopped part way (an error was raised
+    // between the launch and the stream's completion).
+    void ensure_counters(size_t slabs) {
+        if (slabs > counters_zeroed || counters_dirty) {
+            counters.ensure(std::max(slabs, counters_zeroed));
+            counters_zeroed = std::max(slabs, counters_zeroed);
+            VK_HIP(hipMemsetAsync(counters.get(), 0, counters_zeroed * sizeof(unsigned), stream));
+        }
     }
 
     // v0-v3: LUT ([q][s][c]) then the distance matrix of this batch into `dists`.
@@ -445,6 +453,7 @@ struct vk_searcher {
                                       stream));
             });
             clock.settle();
+            counters_dirty = false;
         }
     }
 
@@ -458,6 +467,7 @@ struct vk_searcher {
             const size_t b = std::min(batch, nq - q0);
             run_variant(v, d_q + q0 * d, b, kk, reinterpret_cast<Pair*>(d_out + q0 * kk), t, clock);
             clock.settle();
+            counters_dirty = false;
         }
     }
 };

@@ -62,14 +62,18 @@ struct WaveList {
     // Inserts the wave-uniform pair (x, xi) at its sorted position; entries behind it move one place back.
     __device__ __forceinline__ void insert(float x, int32_t xi, int K) {
         const int lane = __lane_id();
-        int pos = 0;  // number of entries strictly before (x, xi); they form a prefix because the list is sorted
+        // Entries strictly before (x, xi) form a prefix (the list is sorted): those with a smaller distance, plus,
+        // only when some entry has exactly distance x (rare), those equal in distance with a smaller id.
+        int pos = 0;
 #pragma unroll
-        for (int s = 0; s < S; ++s) pos += __popcll(__ballot(pair_less(d[s], id[s], x, xi)));
+        for (int s = 0; s < S; ++s) {
+            pos += __popcll(__builtin_amdgcn_ballot_w64(d[s] < x));
+            if (__builtin_amdgcn_ballot_w64(d[s] == x)) pos += __popcll(__builtin_amdgcn_ballot_w64(d[s] == x && id[s] < xi));
+        }
         float carry_d = 0.f;
         int32_t carry_i = 0;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const int p = s * WAVE + lane;
             float prev_d = wave_shr1(d[s]);
             int32_t prev_i = wave_shr1(id[s]);
             if (s > 0 && lane == 0) {  // lane 0 of a later register takes the last entry of the previous one
@@ -80,9 +84,15 @@ struct WaveList {
                 carry_d = lane_read(d[s], WAVE - 1);
                 carry_i = lane_read(id[s], WAVE - 1);
             }
-            const bool keep = p < pos, here = p == pos;
-            d[s] = keep ? d[s] : (here ? x : prev_d);
-            id[s] = keep ? id[s] : (here ? xi : prev_i);
+            const bool keep = s * WAVE + lane < pos;
+            d[s] = keep ? d[s] : prev_d;
+            id[s] = keep ? id[s] : prev_i;
+            const int at = pos - s * WAVE;  // wave-uniform: the candidate's lane in this register, if any
+            if (at >= 0 && at < WAVE) {
+                const bool here = lane == at;
+                d[s] = here ? x : d[s];
+                id[s] = here ? xi : id[s];
+            }
         }
         refresh(K);
     }
@@ -102,7 +112,13 @@ struct WaveList {
     // uses dist <= threshold as a cheap superset test; the exact (dist, id) test is re-done per candidate
     // because the threshold falls as candidates go in.
     __device__ __forceinline__ void offer(float x, int32_t xi, bool valid, int K) {
-        uint64_t mask = __ballot(valid && x <= thr_d);
+        offer_masked(x, xi, __builtin_amdgcn_ballot_w64(valid), K);
+    }
+
+    // As offer, with the lanes that hold candidates given as a wave-uniform mask: the common no-candidate case is
+    // one compare into a scalar mask and one branch.
+    __device__ __forceinline__ void offer_masked(float x, int32_t xi, uint64_t valid, int K) {
+        uint64_t mask = __builtin_amdgcn_ballot_w64(x <= thr_d) & valid;
         while (mask) {
             const int src = __ffsll(static_cast<unsigned long long>(mask)) - 1;
             mask &= mask - 1;
@@ -136,19 +152,24 @@ __device__ __forceinline__ int count_before(const Pair* l, int K, Pair e, bool s
     return lo;
 }
 
-// Merges L sorted lists of K pairs (lists[l * K + j], in LDS) into their K smallest, written to out[0..K).
-// Rank of an entry = its index in its own list + entries of earlier lists that are <= it + entries of later
-// lists that are < it; ranks are unique even with equal (sentinel) entries. All threads of the block call it;
-// the caller synchronises before (lists written) and after (out read).
-__device__ __forceinline__ void merge_lists(const Pair* lists, int L, int K, Pair* out, int tid, int nthreads) {
+// Merges L sorted lists of K pairs (lists[l * K + j], in LDS) into their `limit` (<= K) smallest, written to
+// out[0..limit) (LDS or global). Rank of an entry = its index in its own list + entries of earlier lists that are
+// <= it + entries of later lists that are < it; ranks are unique even with equal (sentinel) entries. With `pad`,
+// empty slots are written as the reference's {+inf, -1}. All threads of the block call it; the caller
+// synchronises before (lists written) and, for LDS output, after (out read).
+__device__ __forceinline__ void merge_lists(const Pair* lists, int L, int K, Pair* out, int tid, int nthreads,
+                                            int limit, bool pad) {
     for (int t = tid; t < L * K; t += nthreads) {
         const int l = t / K, j = t % K;
         const Pair e = lists[t];
         int rank = j;
-        for (int o = 0; o < L && rank < K; ++o)
+        for (int o = 0; o < L && rank < limit; ++o)
             if (o != l) rank += count_before(lists + o * K, K, e, o > l);
-        if (rank < K) out[rank] = e;
+        if (rank < limit) out[rank] = pad && e.i == kEmptyId ? Pair{INFINITY, -1} : e;
     }
+}
+__device__ __forceinline__ void merge_lists(const Pair* lists, int L, int K, Pair* out, int tid, int nthreads) {
+    merge_lists(lists, L, K, out, tid, nthreads, K, false);
 }
 
 }  // namespace vk

@@ -24,16 +24,22 @@ hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_
 
 // ---- fused scan with wave-cooperative lists (fused_wave_*.hip)
 struct WaveScanArgs {
-    const float* lut;     // [slabs * ng][m][256][qg]
-    const uint4* codes;   // word-interleaved, padded to a multiple of 256 vectors
+    const float* queries;    // nq x d; each block builds its slab's tables from these
+    const float* centroids;  // [m][256][d / m]
+    const uint4* codes;      // word-interleaved, padded to a multiple of 256 vectors
     int64_t n;
+    int d;
     int m;
     int nq;
-    int K;                // list length, <= 64 * S
-    int64_t n_gran;       // granules (64 * ilp vectors) per slab
-    int64_t total;        // slabs * n_gran
-    int max_slots;        // partial lists per slab, upper bound over slabs
-    Pair* part;           // [slabs][max_slots][qg * ng][K]
+    int K;                   // list length, <= 64 * S
+    int k;                   // results per query
+    int64_t n_gran;          // granules (64 * ilp vectors) per slab
+    int64_t total;           // slabs * n_gran
+    int max_slots;           // blocks per slab, upper bound over slabs
+    int lists_per_block;     // partial lists a block writes per (slab, query): one per wave, or 1 (merged in LDS)
+    Pair* part;              // [slabs][qg * ng][max_slots][lists_per_block][K]
+    unsigned* counters;      // [slabs], zero between searches: blocks of a slab that have finished
+    Pair* out;               // [nq][k]; empty slots become {+inf, -1}
 };
 
 struct WaveScanKernel {
