@@ -91,15 +91,12 @@ ThreadScanKernel fused_thread_kernel(int variant, int K, int q, int ilp);
 
 // ---- selection / final merge (select.hip)
 struct SelectArgs {
-    int mode;              // 0: rows of distances, ids = column index; 1: grid partials; 2: balanced-partition partials
+    int mode;              // 0: rows of distances, ids = column index; 1: grid partials
     const float* dists;    // mode 0: [nq][len]
     int64_t len;
-    const Pair* part;      // modes 1, 2
+    const Pair* part;      // mode 1
     int K;                 // list length of the selection (and of each partial list)
     int64_t bx;            // mode 1: partial lists per query, layout [q][bx][K]
-    int qs;                // mode 2: queries per slab
-    int max_slots;         // mode 2
-    int64_t n_gran, total, grid;  // mode 2 partition
     int k;                 // results written per query
     Pair* out;             // [nq][k]; empty slots become {+inf, -1}
 };

@@ -1,10 +1,9 @@
 // Top-k selection (reference: select_kernel, kernels.cuh:179-202, launched by searcher.cu:285-296).
 // One block per query. Each wave streams its share of the candidates into a wave-cooperative sorted list
-// (threshold test per candidate, rare inserts), then the four wave lists are merged by rank. Three candidate
+// (threshold test per candidate, rare inserts), then the four wave lists are merged by rank. Two candidate
 // sources share the kernel:
 //   mode 0 — a row of n distances, ids are column indices (unfused scans);
-//   mode 1 — bx partial K-lists per query laid out [q][bx][K] (per-thread-list fused scans);
-//   mode 2 — partial K-lists of the balanced partition of the wave-list scan, [slab][slot][query][K].
+//   mode 1 — bx partial K-lists per query laid out [q][bx][K] (per-thread-list fused scans).
 // Empty slots ({+inf, INT32_MAX}) are skipped, like the reference skips id < 0, and the output turns any that
 // remain into {+inf, -1}.
 #include "kernels.hpp"
@@ -30,25 +29,12 @@ __global__ void __launch_bounds__(256) select_kernel(SelectArgs a) {
             list.offer(x, static_cast<int32_t>(j), valid, K);
         }
     } else {
-        const Pair* first;
-        int64_t count, stride;
-        if (a.mode == 1) {
-            first = a.part + q * a.bx * K;
-            count = a.bx;
-            stride = K;
-        } else {
-            const int64_t slab = q / a.qs, qq = q % a.qs;
-            const int64_t lo = first_block_of(slab * a.n_gran, a.grid, a.total);
-            const int64_t hi = first_block_of((slab + 1) * a.n_gran - 1, a.grid, a.total);
-            count = hi - lo + 1;
-            first = a.part + (slab * a.max_slots * a.qs + qq) * K;
-            stride = static_cast<int64_t>(a.qs) * K;
-        }
-        const int64_t all = count * K;
+        const Pair* first = a.part + q * a.bx * K;
+        const int64_t all = a.bx * K;
         for (int64_t base = static_cast<int64_t>(wave) * WAVE; base < all; base += W * WAVE) {
             const int64_t e = base + lane;
             Pair p{INFINITY, kEmptyId};
-            if (e < all) p = first[(e / K) * stride + e % K];
+            if (e < all) p = first[e];
             list.offer(p.d, p.i, p.i != kEmptyId, K);
         }
     }
