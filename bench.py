@@ -14,8 +14,11 @@ Prints ONE JSON line on stdout (progress goes to stderr):
                absent, the oracle port, on a bounded sample of the same queries on this host's cores
   parity       the GPU results for the CPU sample compared with the CPU results (ids and distance bits)
 
+--variant v9 runs the fp16-table search (FusedWarpF16): its parity is against the CPU restatement of the fp16
+arithmetic, and `recall_delta` reports how much of the fp32 reference's top-k it returns.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config B|A|C32|C64|D|D1|E] [--queries-per-block Q]
-                       [--ilp U] [--variant v8] [--no-cpu] [--no-recall]
+                       [--ilp U] [--variant v8|v9|...] [--no-cpu] [--no-recall]
 """
 from __future__ import annotations
 
@@ -210,17 +213,21 @@ def main():
     achieved = lookups / (scan_ms * 1e-3)
     q_eff = shape.queries_per_block
     hbm_bytes = float(n) * m * math.ceil(nq / q_eff)
+    f16 = variant == vk.ScanVariant.FusedWarpF16
+    # fp16 tables: a read of 2*Q bytes serves Q queries, so the floor is twice the fp32 floor of the same read width
+    peak = (2 * floors[q_eff // 2] if q_eff >= 2 else floors[1]) if f16 else floors[best_qg]
     roofline = {
         "bound": "lds",
         "achieved": achieved / 1e12,
-        "peak": floors[best_qg] / 1e12,
+        "peak": peak / 1e12,
         "unit": "Tlookup/s",
-        "frac": achieved / floors[best_qg],
+        "frac": achieved / peak,
         "traffic": (load_traffic(args.config) or {}).get("bytes_per_launch"),
         "traffic_detail": load_traffic(args.config),
         "kernel": "fused_wave_kernel_t (scan + per-wave top-k)",
         "kernel_ms": scan_ms,
-        "algorithmic": f"n*m*nq = {lookups:.3e} LDS lookups per launch (one 4-byte table read + one fp32 add each)",
+        "algorithmic": f"n*m*nq = {lookups:.3e} LDS lookups per launch (one {2 if f16 else 4}-byte table read + "
+                       f"one fp32 add each)",
         "floor_by_table_width": {f"b{32 * q}_Q{q}": floors[q] / 1e12 for q in floors},
         "hbm": {"achieved_gbs": hbm_bytes / (scan_ms * 1e-3) / 1e9, "peak_gbs": HBM_PEAK_GBS,
                 "frac": hbm_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "measured_read_gbs": hbm_gbs,
@@ -239,7 +246,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": qps / A100_V8_QPS if args.config == "B" else None,
-        "dtype": "f32",
+        "dtype": "f16 tables, f32 sums" if f16 else "f32",
         "data": ("synthetic: seeded 1000-component Gaussian mixture (sigma 0.3), PQ trained by seeded k-means"
                  if data == "mixture" else "synthetic: seeded uniform codes, N(0,1) codebooks and queries"),
         "config": {"workload": desc, "n": n, "d": d, "m": m, "nq": nq, "k": k, "variant": vk.variant_name(variant),
@@ -261,10 +268,21 @@ def main():
         rec, res = cpu_baseline(centroids, codes, queries, k, d)
         record["cpu_baseline"] = rec
         sample = res.shape[0]
+        against = rec["kind"]
+        if f16:
+            # fp16 tables are checked against their own restatement; the fp32 reference gives the recall delta
+            from oracle import binding as orc
+            overlap = float(np.mean([len(set(res["id"][q]) & set(out["id"][q])) / k for q in range(sample)]))
+            record["recall_delta"] = {"queries": sample, "topk_overlap_with_fp32_reference": overlap,
+                                      "note": "fraction of the fp32 CPU reference's top-k ids that the fp16-table "
+                                              "search also returns"}
+            log(f"[bench] fp16 tables: top-{k} overlap with the fp32 reference {overlap:.4f}")
+            res = orc.adc_search_f16(centroids, d, codes, queries[:sample], k)
+            against = "oracle fp16-table restatement"
         same_ids = bool((res["id"] == out[:sample]["id"]).all())
         same_bits = bool((res["dist"].view(np.uint32) == out[:sample]["dist"].view(np.uint32)).all())
         record["parity"] = {"queries": sample, "ids_identical": same_ids, "dist_bits_identical": same_bits,
-                            "against": rec["kind"]}
+                            "against": against}
         log(f"[bench] CPU {rec['kind']}: {rec['value']:.1f} queries/s on {rec['cores']} threads; parity ids "
             f"{same_ids} dist bits {same_bits}")
     else:

@@ -23,6 +23,7 @@ enum class ScanVariant {
     FusedVec,      // v6: v5 + 16-byte-word interleaved layout (m % 16 == 0)
     FusedVecMQ,    // v7: v6 + Q queries per block sharing every code load (m % 16 == 0)
     FusedWarp,     // v8: one wave-cooperative list per (wave, query), query-interleaved LDS tables
+    FusedWarpF16,  // v9 (not in the reference): v8 with fp16 LDS tables, up to 8 queries per 16-byte read
 };
 
 const char* variant_name(ScanVariant v);

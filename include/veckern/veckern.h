@@ -34,7 +34,11 @@ enum vk_status {
     VK_ERR_OUT_OF_MEMORY = 5     /* device allocation failed */
 };
 
-/* Scan variants: values and order of veckern::gpu::ScanVariant (gpu.hpp:13-23). */
+/* Scan variants: values and order of veckern::gpu::ScanVariant (gpu.hpp:13-23), plus one of this build's own:
+ * VK_V9_FUSED_WARP_F16 is v8 with binary16 LDS tables (each query's fp32 entries scaled by a power of two so the
+ * largest lies in [2^14, 2^15), rounded to nearest even; sums in fp32 and scaled back exactly). It is the
+ * reference's "lower-precision tables" next step (README.md:219): distances differ from v8's by the table rounding
+ * (relative error of order 1e-3), so results can differ from the fp32 path where candidates are that close. */
 enum vk_variant {
     VK_V0_GLOBAL_LUT = 0,
     VK_V1_SHARED_LUT = 1,
@@ -45,7 +49,8 @@ enum vk_variant {
     VK_V6_FUSED_VEC = 6,
     VK_V7_FUSED_VEC_MQ = 7,
     VK_V8_FUSED_WARP = 8,
-    VK_NUM_VARIANTS = 9
+    VK_V9_FUSED_WARP_F16 = 9,
+    VK_NUM_VARIANTS = 10
 };
 
 /* Same layout as veckern::Neighbor (common.hpp:13-16): ascending (dist, id); padding is {+inf, -1}. */

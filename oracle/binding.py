@@ -37,6 +37,11 @@ def oracle() -> ctypes.CDLL:
         lib.vko_recall_at_k.argtypes = [_P, _S, _P, _S, _S, _S]
         lib.vko_max_threads.restype = ctypes.c_int
         lib.vko_topk_run.argtypes = [_P, _P, _S, _S, _P]
+        lib.vko_f32_to_f16_array.argtypes = [_P, _S, _P]
+        lib.vko_f16_to_f32_array.argtypes = [_P, _S, _P]
+        lib.vko_table_shift.restype = ctypes.c_int
+        lib.vko_table_shift.argtypes = [_P, _S]
+        lib.vko_adc_search_f16.argtypes = [_P, _S, _S, _P, _S, _P, _S, _S, _P]
         _oracle = lib
     return _oracle
 
@@ -112,6 +117,39 @@ def adc_search(centroids: np.ndarray, d: int, codes: np.ndarray, queries: np.nda
     if rc != 0:
         raise ValueError("vko_adc_search rejected its input")
     return out
+
+
+def adc_search_f16(centroids: np.ndarray, d: int, codes: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
+    """The fp16-table search (ScanVariant.FusedWarpF16) restated on the CPU."""
+    codes = _c(codes, np.uint8)
+    n, m = codes.shape
+    q = _c(queries, np.float32).reshape(-1, d)
+    c = _c(centroids, np.float32)
+    out = np.empty((q.shape[0], k), dtype=NEIGHBOR)
+    rc = oracle().vko_adc_search_f16(c.ctypes.data, d, m, codes.ctypes.data, n, q.ctypes.data, q.shape[0], k,
+                                     out.ctypes.data)
+    if rc != 0:
+        raise ValueError("vko_adc_search_f16 rejected its input")
+    return out
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    oracle().vko_f32_to_f16_array(x.ctypes.data, x.size, out.ctypes.data)
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    oracle().vko_f16_to_f32_array(h.ctypes.data, h.size, out.ctypes.data)
+    return out
+
+
+def table_shift(table: np.ndarray) -> int:
+    t = _c(table, np.float32)
+    return oracle().vko_table_shift(t.ctypes.data, t.size)
 
 
 def recall_at_k(found: np.ndarray, truth: np.ndarray, k: int) -> float:

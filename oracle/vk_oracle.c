@@ -165,6 +165,117 @@ int vko_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* co
     return failed ? -1 : 0;
 }
 
+/* ---- binary16 (IEEE 754-2008): sign bit 15, exponent bits 14-10 (bias 15), fraction bits 9-0. */
+static uint32_t f32_bits(float x) {
+    uint32_t b;
+    memcpy(&b, &x, sizeof b);
+    return b;
+}
+
+static float f32_from_bits(uint32_t b) {
+    float x;
+    memcpy(&x, &b, sizeof x);
+    return x;
+}
+
+uint16_t vko_f32_to_f16(float x) {
+    const uint32_t b = f32_bits(x);
+    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    const uint32_t a = b & 0x7fffffffu;
+    if (a >= 0x7f800000u) /* infinity, or NaN with its top fraction bits kept and the quiet bit set */
+        return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x0200u | ((a >> 13) & 0x03ffu) : 0u));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: rounds past the largest finite, 65504 */
+    if (a >= 0x38800000u) { /* normal binary16 (>= 2^-14): drop 13 fraction bits, round to nearest even */
+        uint32_t h = ((a >> 23) - 127u + 15u) << 10 | ((a >> 13) & 0x03ffu);
+        const uint32_t rest = a & 0x1fffu;
+        if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h; /* a carry into the exponent is correct */
+        return (uint16_t)(sign | h);
+    }
+    if (a < 0x33000000u) return sign; /* below 2^-25: rounds to zero (2^-25 itself is handled below, to even 0) */
+    { /* subnormal binary16: units of 2^-24; the f32 value is mant * 2^(e - 23), e in [-25, -15] */
+        const int e = (int)(a >> 23) - 127;
+        const uint32_t mant = (a & 0x007fffffu) | 0x00800000u;
+        const int drop = -e - 1; /* 14 .. 24 */
+        uint32_t h = mant >> drop;
+        const uint32_t rest = mant & ((1u << drop) - 1u), half = 1u << (drop - 1);
+        if (rest > half || (rest == half && (h & 1u))) ++h;
+        return (uint16_t)(sign | h);
+    }
+}
+
+float vko_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, frac = h & 0x03ffu;
+    if (e == 31u) return f32_from_bits(sign | 0x7f800000u | frac << 13);
+    if (e != 0u) return f32_from_bits(sign | (e - 15u + 127u) << 23 | frac << 13);
+    if (frac == 0u) return f32_from_bits(sign);
+    /* subnormal: frac * 2^-24, normalised for f32 */
+    int exp = -14;
+    uint32_t f = frac;
+    while (!(f & 0x0400u)) {
+        f <<= 1;
+        --exp;
+    }
+    return f32_from_bits(sign | (uint32_t)(exp + 127) << 23 | (f & 0x03ffu) << 13);
+}
+
+void vko_f32_to_f16_array(const float* x, size_t count, uint16_t* out) {
+    for (size_t i = 0; i < count; ++i) out[i] = vko_f32_to_f16(x[i]);
+}
+
+void vko_f16_to_f32_array(const uint16_t* h, size_t count, float* out) {
+    for (size_t i = 0; i < count; ++i) out[i] = vko_f16_to_f32(h[i]);
+}
+
+int vko_table_shift(const float* table, size_t count) {
+    uint32_t mx = 0;
+    for (size_t i = 0; i < count; ++i) {
+        const uint32_t b = f32_bits(table[i]);
+        if (b > mx) mx = b; /* entries are >= +0, so the bit order is the value order (NaN above +inf) */
+    }
+    if (mx == 0u || mx >= 0x7f800000u) return 0;
+    int e;
+    if (mx >= 0x00800000u) {
+        e = (int)(mx >> 23) - 127;
+    } else { /* subnormal: the position of the highest set bit */
+        e = -150;
+        for (uint32_t v = mx; v; v >>= 1) ++e;
+    }
+    return e - 14;
+}
+
+int vko_adc_search_f16(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n, const float* queries,
+                       size_t nq, size_t k, vko_neighbor* out) {
+    if (m == 0 || d == 0 || d % m != 0) return -1;
+    int failed = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (long long q = 0; q < (long long)nq; ++q) {
+        float* lut = (float*)malloc(m * VKO_KSUB * sizeof(float));
+        vko_topk top;
+        if (!lut || vko_topk_init(&top, k) != 0) {
+            free(lut);
+            failed = 1;
+            continue;
+        }
+        vko_compute_lut(centroids, d, m, queries + (size_t)q * d, 1, lut);
+        const int shift = vko_table_shift(lut, m * VKO_KSUB);
+        for (size_t j = 0; j < m * VKO_KSUB; ++j) lut[j] = vko_f16_to_f32(vko_f32_to_f16(ldexpf(lut[j], -shift)));
+        for (size_t i = 0; i < n; ++i) {
+            const uint8_t* code = codes + i * m;
+            float acc = 0.f;
+            for (size_t s = 0; s < m; ++s) acc += lut[s * VKO_KSUB + code[s]];
+            vko_topk_push(&top, acc, (int32_t)i);
+        }
+        vko_neighbor* res = out + (size_t)q * k;
+        vko_topk_write(&top, res);
+        for (size_t j = 0; j < k; ++j)
+            if (res[j].id >= 0) res[j].dist = ldexpf(res[j].dist, shift);
+        vko_topk_free(&top);
+        free(lut);
+    }
+    return failed ? -1 : 0;
+}
+
 /* ---- cpu_ref.cpp:79-91: truth[:k] is treated as a set; every found id that is in it counts as a hit. */
 double vko_recall_at_k(const vko_neighbor* found, size_t found_stride, const int32_t* truth, size_t truth_stride,
                        size_t nq, size_t k) {

@@ -16,12 +16,23 @@
  *   vko_adc_search      src/cpu/cpu_ref.cpp:38-54          LUT + scan + top-k per query, OpenMP over queries
  *   vko_recall_at_k     src/cpu/cpu_ref.cpp:79-91          mean |found[:k] ∩ set(truth[:k])| / k
  *
+ * The fp16-table search (ScanVariant::FusedWarpF16, this build's own variant; the reference lists lower-precision
+ * tables as a next step, README.md:219) is restated on top of the same LUT:
+ *   vko_f32_to_f16 / vko_f16_to_f32   IEEE 754 binary16 conversion, round to nearest even (from the format's
+ *                                     definition: 1 sign, 5 exponent, 10 fraction bits, subnormals kept)
+ *   vko_table_shift     per-query power of two bringing the largest LUT entry into [2^14, 2^15)
+ *   vko_adc_search_f16  LUT -> scaled and rounded to binary16 -> the fp32 sequential scan of cpu_ref.cpp:46-49
+ *                       -> top-k -> distances scaled back by the power of two
+ *
  * Pinning (how each function is checked, in tests/test_oracle.py):
  *   - against the reference's own CPU sources compiled into oracle/_ref (bit-exact), when that library is built;
  *   - against the committed golden fixtures in tests/golden/ (written from oracle/_ref);
  *   - against the reference's known-answer tests (tests/test_cpu.cpp:33-46) and invariants
  *     (ADC == exact L2 to the decoded vector, tests/test_cpu.cpp:58-67; staged == fused, :84-94);
- *   - against brute force (full sort of all (dist, id) pairs) and numpy float32 on small inputs.
+ *   - against brute force (full sort of all (dist, id) pairs) and numpy float32 on small inputs;
+ *   - fp16: the conversions against numpy's float16 (every binary16 value, every midpoint between neighbours,
+ *     random bit patterns); the search against a numpy restatement, and equal to the fp32 search when every
+ *     scaled entry is exactly representable.
  * No function is left unpinned.
  *
  * Build flags matter for bit-exactness: -O3 -ffp-contract=off, no -march and no -ffast-math, so that no FMA
@@ -75,6 +86,20 @@ double vko_recall_at_k(const vko_neighbor* found, size_t found_stride, const int
 /* Pushes (dists[j], ids[j]) for j < count into a top-k of size k and writes its k results (test helper for the
  * TopK known-answer tests, cpu_ref.hpp:14-40). */
 void vko_topk_run(const float* dists, const int32_t* ids, size_t count, size_t k, vko_neighbor* out);
+/* IEEE binary16 bits of x, rounded to nearest even; overflow gives infinity, NaN stays NaN (quiet). */
+uint16_t vko_f32_to_f16(float x);
+/* The float value of binary16 bits h (exact). */
+float vko_f16_to_f32(uint16_t h);
+/* Element-wise forms of the two conversions over count values. */
+void vko_f32_to_f16_array(const float* x, size_t count, uint16_t* out);
+void vko_f16_to_f32_array(const uint16_t* h, size_t count, float* out);
+/* Exponent e applied to one query's table (entries scaled by 2^-e): with E = floor(log2(largest entry)),
+ * e = E - 14; 0 when the largest entry is 0, infinite or NaN. */
+int vko_table_shift(const float* table, size_t count);
+/* fp16-table search: per query, the fp32 LUT of vko_compute_lut, each entry scaled by 2^-e and rounded to
+ * binary16, the sequential fp32 scan, top-k, and the k distances scaled by 2^e. out: nq x k. */
+int vko_adc_search_f16(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n, const float* queries,
+                       size_t nq, size_t k, vko_neighbor* out);
 /* Threads the OpenMP loops above will use. */
 int vko_max_threads(void);
 

@@ -27,6 +27,16 @@ CASE("effective_q halves Q until the tables fit and, for per-thread lists, Q*K <
     EXPECT(effective_q(8, 160, lds, false, 8) == 1);
 }
 
+CASE("cap_q_by_batch keeps no more query slots than the batch needs") {
+    EXPECT(cap_q_by_batch(4, 1) == 1);
+    EXPECT(cap_q_by_batch(4, 2) == 2);
+    EXPECT(cap_q_by_batch(4, 3) == 4);
+    EXPECT(cap_q_by_batch(8, 5) == 8);
+    EXPECT(cap_q_by_batch(8, 4) == 4);
+    EXPECT(cap_q_by_batch(4, 1000) == 4);
+    EXPECT(cap_q_by_batch(1, 1) == 1);
+}
+
 CASE("blocks_x_waves reproduces the reference's recorded launch shapes") {
     const int64_t wave = 4 * 108;  // A100: 4 resident blocks per SM x 108 SMs
     // tests/test_gpu.cpp fixture, v7 Q=2 T=128: run_all.log:28 "blocks_x=22 grid_y=19 ... waves=0.97"

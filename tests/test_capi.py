@@ -68,10 +68,11 @@ def test_product_libraries_do_not_link_the_oracle():
 def test_variant_registry():
     names = [vk.variant_name(v) for v in vk.ScanVariant]
     assert names == ["v0_global_lut", "v1_shared_lut", "v2_shared_lut_vec", "v3_interleaved", "v4_fused",
-                     "v5_fused_reg", "v6_fused_vec", "v7_fused_vec_mq", "v8_fused_warp"]
-    assert [vk.is_fused(v) for v in vk.ScanVariant] == [False] * 4 + [True] * 5
-    assert [vk.needs_m16(v) for v in vk.ScanVariant] == [False, False, True, False, False, False, True, True, True]
-    assert vk.variant_name(9) == "unknown" and vk.variant_name(-1) == "unknown"
+                     "v5_fused_reg", "v6_fused_vec", "v7_fused_vec_mq", "v8_fused_warp", "v9_fused_warp_f16"]
+    assert [vk.is_fused(v) for v in vk.ScanVariant] == [False] * 4 + [True] * 6
+    assert [vk.needs_m16(v) for v in vk.ScanVariant] == [False, False, True, False, False, False, True, True, True,
+                                                         True]
+    assert vk.variant_name(10) == "unknown" and vk.variant_name(-1) == "unknown"
 
 
 def test_tuning_defaults_and_validation():

@@ -241,3 +241,102 @@ def test_planted_mistakes_fail_the_checks():
     good = b.adc_search(z["centroids"], d, z["codes"], z["queries"], 10)
     assert not ((good["id"] + 1) == z["search_k10_id"]).all()
     del c64, q64
+
+
+# ---------------------------------------------------------------- 5. the fp16-table search (FusedWarpF16)
+
+def _same_f32(got, exp):
+    """Bit equality, with any NaN matching any NaN (payloads are not specified by the format)."""
+    gn, en = np.isnan(got), np.isnan(exp)
+    return (gn == en).all() and (bits(got)[~gn] == bits(exp)[~en]).all()
+
+
+def test_f16_to_f32_matches_numpy_for_every_binary16_value():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    assert _same_f32(b.f16_bits_to_f32(h), h.view(np.float16).astype(np.float32))
+
+
+def test_f32_to_f16_matches_numpy_round_to_nearest_even():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    vals = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(vals)
+    # every binary16 value converts back to itself
+    assert (b.f32_to_f16_bits(vals[finite]) == h[finite]).all()
+    # every midpoint between neighbouring finite values (exact in f32), and one f32 ulp either side of it
+    pos = np.sort(vals[finite & (vals >= 0)]).astype(np.float64)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
+    probe = np.concatenate([mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0)),
+                            np.float32([65504, 65519.996, 65520, 65536, 1e9, 2.0**-24, 2.0**-25, 3 * 2.0**-26,
+                                        2.0**-26, 1e-30, 0.0])])
+    probe = np.concatenate([probe, -probe])
+    with np.errstate(over="ignore"):
+        exp = probe.astype(np.float16).view(np.uint16)
+    assert (b.f32_to_f16_bits(probe) == exp).all()
+    # random bit patterns over the whole f32 range
+    rnd = np.random.default_rng(31).integers(0, 1 << 32, size=1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        exp = rnd.astype(np.float16)
+    got = b.f32_to_f16_bits(rnd).view(np.float16)
+    assert _same_f32(got.astype(np.float32), exp.astype(np.float32))
+
+
+def test_table_shift_closed_forms():
+    f = lambda *v: b.table_shift(np.float32(v))
+    assert f(0.0, 0.0) == 0
+    assert f(1.0) == -14 and f(1.5, 0.25) == -14
+    assert f(2.0**14) == 0 and f(3.0, 65504.0) == 1
+    assert f(2.0**-149) == -149 - 14 and f(2.0**-127, 0.0) == -127 - 14
+    assert f(np.inf, 1.0) == 0 and f(np.nan, 1.0) == 0
+
+
+def numpy_search_f16(cent, d, codes, queries, k):
+    """numpy restatement of the fp16-table search: float32 LUT, np.frexp for the exponent, np.ldexp scaling,
+    numpy's float16 rounding, a float32 scan in sub-space order, (dist, id) sort, exact scaling back."""
+    lut = numpy_lut(cent, queries)
+    out = np.zeros((queries.shape[0], k), dtype=b.NEIGHBOR)
+    for q in range(queries.shape[0]):
+        mx = lut[q].max()
+        shift = 0 if (mx == 0 or not np.isfinite(mx)) else int(np.frexp(mx)[1]) - 1 - 14
+        with np.errstate(over="ignore"):
+            t = np.ldexp(lut[q], -shift).astype(np.float32).astype(np.float16).astype(np.float32)
+        acc = np.zeros(codes.shape[0], dtype=np.float32)
+        for s in range(codes.shape[1]):
+            acc = (acc + t[s, codes[:, s]]).astype(np.float32)
+        order = np.lexsort((np.arange(codes.shape[0]), acc))[:k]
+        out[q]["dist"] = np.ldexp(acc[order], shift).astype(np.float32)
+        out[q]["id"] = order
+    return out
+
+
+@pytest.mark.parametrize("scale", [1.0, 300.0, 1e-6])
+def test_search_f16_equals_numpy_restatement(scale):
+    cent, codes, queries = random_case(32, 3000, 32, 8, 5, "normal")
+    cent, queries = (cent * scale).astype(np.float32), (queries * scale).astype(np.float32)
+    got = b.adc_search_f16(cent, 32, codes, queries, 17)
+    exp = numpy_search_f16(cent, 32, codes, queries, 17)
+    assert (got["id"] == exp["id"]).all() and (bits(got["dist"]) == bits(exp["dist"])).all()
+
+
+def test_search_f16_equals_fp32_search_when_tables_are_exact():
+    # small-integer data: every LUT entry is an integer below 2^11, so scaling by a power of two and rounding to
+    # binary16 are exact, every sum is exact, and the fp16 search must return the fp32 search's bits
+    cent, codes, queries = random_case(33, 4000, 64, 16, 6, "ties")
+    f16 = b.adc_search_f16(cent, 64, codes, queries, 25)
+    f32 = b.adc_search(cent, 64, codes, queries, 25)
+    assert (f16["id"] == f32["id"]).all() and (bits(f16["dist"]) == bits(f32["dist"])).all()
+
+
+def test_planted_fp16_mistakes_fail_the_checks():
+    # rounding by truncation instead of to nearest even
+    x = np.float32([1.0 + 2.0**-11 + 2.0**-20, 3.0 + 3 * 2.0**-11])
+    trunc = (x.view(np.uint32) >> 13 & 0x3ff) | ((x.view(np.uint32) >> 23) - 112) << 10
+    assert not (b.f32_to_f16_bits(x) == trunc.astype(np.uint16)).all()
+    # no per-query scaling: large-valued tables overflow binary16 and the results change
+    cent, codes, queries = random_case(34, 2000, 32, 8, 3, "normal")
+    cent, queries = (cent * 300).astype(np.float32), (queries * 300).astype(np.float32)
+    lut = b.compute_lut(cent, 32, 8, queries)
+    with np.errstate(over="ignore"):
+        unscaled = lut.astype(np.float16).astype(np.float32)
+    assert np.isinf(unscaled).any()
+    good = b.adc_search_f16(cent, 32, codes, queries, 10)
+    assert np.isfinite(good["dist"]).all()

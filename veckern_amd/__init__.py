@@ -44,7 +44,7 @@ class VkLogicError(VkError):
 
 
 class ScanVariant(enum.IntEnum):
-    """veckern::gpu::ScanVariant (reference gpu.hpp:13-23)."""
+    """veckern::gpu::ScanVariant (reference gpu.hpp:13-23); FusedWarpF16 is this build's fp16-table v8."""
 
     GlobalLut = 0
     SharedLut = 1
@@ -55,6 +55,7 @@ class ScanVariant(enum.IntEnum):
     FusedVec = 6
     FusedVecMQ = 7
     FusedWarp = 8
+    FusedWarpF16 = 9
 
 
 class _Neighbor(ctypes.Structure):

@@ -21,13 +21,25 @@
 #define VK_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace vk {
-// Per-m instance tables of the wave-list scan (fused_wave_m*.hip).
+// Per-m instance tables of the wave-list scan, fp32 (fused_wave_m*.hip) and fp16 tables (fused_wave_h*.hip).
 WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments);
 WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments);
 WaveScanKernel fused_wave_kernel_m64(int qg, int ng, int ilp, int segments);
 WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_h16(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_h32(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_h64(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_hx(int qg, int ng, int ilp, int segments);
 
-WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments) {
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16) {
+    if (f16) {
+        switch (m) {
+            case 16: return fused_wave_kernel_h16(qg, ng, ilp, segments);
+            case 32: return fused_wave_kernel_h32(qg, ng, ilp, segments);
+            case 64: return fused_wave_kernel_h64(qg, ng, ilp, segments);
+            default: return fused_wave_kernel_hx(qg, ng, ilp, segments);
+        }
+    }
     switch (m) {
         case 16: return fused_wave_kernel_m16(qg, ng, ilp, segments);
         case 32: return fused_wave_kernel_m32(qg, ng, ilp, segments);
@@ -220,17 +232,20 @@ struct vk_searcher {
         VK_HIP(hipStreamSynchronize(stream));
     }
 
-    // v8: the wave-list scan over the balanced partition, then the final merge. d_q: device queries of this
-    // batch; writes b x kk results to d_out.
-    void run_wave(const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
+    // v8 / v9 (f16 tables): the wave-list scan over the balanced partition with its final merge, one launch.
+    // d_q: device queries of this batch; writes b x kk results to d_out.
+    void run_wave(const float* d_q, size_t b, size_t kk, bool f16, Pair* d_out, vk_timings* t, StageClock& clock) {
         const int K = vk::plan::dispatched_k(kk);
         const int segments = K <= vk::WAVE ? 1 : 2;
-        const int q = vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, false, K);
-        const int qg = q == 8 ? 4 : q, ng = q == 8 ? 2 : 1;
+        const size_t entry_bytes = f16 ? 2 : sizeof(float);
+        const int q = vk::plan::cap_q_by_batch(
+            vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, false, K, entry_bytes), b);
+        // fp32: 8 queries are two groups of 4 (16-byte reads); fp16: up to 8 queries in one group.
+        const int qg = (!f16 && q == 8) ? 4 : q, ng = (!f16 && q == 8) ? 2 : 1;
         const int ilp = tuning.vectors_per_step;
-        const vk::WaveScanKernel kern = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments);
+        const vk::WaveScanKernel kern = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments, f16);
         if (!kern.fn) fail(VK_ERR_LOGIC, "no fused-warp kernel built for this (Q, ILP, m, K)");
-        const size_t tables = static_cast<size_t>(q) * m * vk::KSUB * sizeof(float);
+        const size_t tables = static_cast<size_t>(q) * m * vk::KSUB * entry_bytes;
         require(tables <= info.max_smem_per_block, "LUT does not fit in LDS");
         const size_t smem = kern.dynamic_lds ? tables : 0;  // fixed-m instances hold the tables in static LDS
         if (kern.dynamic_lds)
@@ -385,7 +400,8 @@ struct vk_searcher {
     }
 
     void run_variant(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
-        if (v == VK_V8_FUSED_WARP) return run_wave(d_q, b, kk, d_out, t, clock);
+        if (v == VK_V8_FUSED_WARP || v == VK_V9_FUSED_WARP_F16)
+            return run_wave(d_q, b, kk, v == VK_V9_FUSED_WARP_F16, d_out, t, clock);
         if (vk_is_fused(v)) return run_thread(v, d_q, b, kk, d_out, t, clock);
         run_unfused(v, d_q, b, kk, d_out, t, clock);
     }
@@ -482,14 +498,16 @@ VK_EXPORT int vk_abi_version(void) { return VK_ABI_VERSION; }
 VK_EXPORT const char* vk_variant_name(int v) {
     static const char* const names[VK_NUM_VARIANTS] = {"v0_global_lut", "v1_shared_lut", "v2_shared_lut_vec",
                                                        "v3_interleaved", "v4_fused",      "v5_fused_reg",
-                                                       "v6_fused_vec",  "v7_fused_vec_mq", "v8_fused_warp"};
+                                                       "v6_fused_vec",  "v7_fused_vec_mq", "v8_fused_warp",
+                                                       "v9_fused_warp_f16"};
     return valid_variant(v) ? names[v] : "unknown";
 }
 
-VK_EXPORT int vk_is_fused(int v) { return v >= VK_V4_FUSED && v <= VK_V8_FUSED_WARP; }
+VK_EXPORT int vk_is_fused(int v) { return v >= VK_V4_FUSED && v <= VK_V9_FUSED_WARP_F16; }
 
 VK_EXPORT int vk_needs_m16(int v) {
-    return v == VK_V2_SHARED_LUT_VEC || v == VK_V6_FUSED_VEC || v == VK_V7_FUSED_VEC_MQ || v == VK_V8_FUSED_WARP;
+    return v == VK_V2_SHARED_LUT_VEC || v == VK_V6_FUSED_VEC || v == VK_V7_FUSED_VEC_MQ || v == VK_V8_FUSED_WARP ||
+           v == VK_V9_FUSED_WARP_F16;
 }
 
 VK_EXPORT void vk_tuning_default(vk_tuning* out) {

@@ -154,18 +154,22 @@ __device__ __forceinline__ int count_before(const Pair* l, int K, Pair e, bool s
 
 // Merges L sorted lists of K pairs (lists[l * K + j], in LDS) into their `limit` (<= K) smallest, written to
 // out[0..limit) (LDS or global). Rank of an entry = its index in its own list + entries of earlier lists that are
-// <= it + entries of later lists that are < it; ranks are unique even with equal (sentinel) entries. With `pad`,
-// empty slots are written as the reference's {+inf, -1}. All threads of the block call it; the caller
-// synchronises before (lists written) and, for LDS output, after (out read).
+// <= it + entries of later lists that are < it; ranks are unique even with equal (sentinel) entries. With `pad`
+// (final results), empty slots are written as the reference's {+inf, -1} and distances are scaled by 2^shift
+// (exact; fp16-table sums). All threads of the block call it; the caller synchronises before (lists written) and,
+// for LDS output, after (out read).
 __device__ __forceinline__ void merge_lists(const Pair* lists, int L, int K, Pair* out, int tid, int nthreads,
-                                            int limit, bool pad) {
+                                            int limit, bool pad, int shift = 0) {
     for (int t = tid; t < L * K; t += nthreads) {
         const int l = t / K, j = t % K;
         const Pair e = lists[t];
         int rank = j;
         for (int o = 0; o < L && rank < limit; ++o)
             if (o != l) rank += count_before(lists + o * K, K, e, o > l);
-        if (rank < limit) out[rank] = pad && e.i == kEmptyId ? Pair{INFINITY, -1} : e;
+        if (rank < limit) {
+            if (pad && e.i == kEmptyId) out[rank] = Pair{INFINITY, -1};
+            else out[rank] = Pair{pad && shift ? ldexpf(e.d, shift) : e.d, e.i};
+        }
     }
 }
 __device__ __forceinline__ void merge_lists(const Pair* lists, int L, int K, Pair* out, int tid, int nthreads) {

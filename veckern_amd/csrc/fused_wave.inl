@@ -1,55 +1,111 @@
 // Fused PQ scan + top-k with one wave-cooperative sorted list per (wave, query): the ScanVariant::FusedWarp
-// path (reference: kernels.cuh:392-526, launch searcher.cu:365-415), designed for gfx950.
+// path (reference: kernels.cuh:392-526, launch searcher.cu:365-415), designed for gfx950, and its fp16-table
+// counterpart FusedWarpF16.
 //
 // Work decomposition. Queries are packed into slabs of QG*NG queries whose lookup tables sit together in LDS.
 // A slab's work is its n vectors cut into granules of 64*U vectors (one wave step). The slabs * n_gran work
 // items are split into `grid` equal contiguous ranges, one per block, with grid = resident blocks on the
 // device (occupancy API), so every CU gets the same number of items and no tail wave is left. A block builds
 // the tables of each slab its range touches directly in LDS from the queries and the codebook (no LUT in HBM),
-// and each (block, slab) pair emits one partial K-list per query. The last block to finish a slab (a per-slab
+// and each (block, slab) pair emits partial K-lists per query. The last block to finish a slab (a per-slab
 // counter) merges the slab's partial lists into the final results, so a search is a single launch.
 //
-// LDS tables. A group of QG queries shares one table laid out [s][c][QG] floats, so a single ds_read_b32 /
-// b64 / b128 at ((s * 256 + c) * QG) returns the entries of all QG queries for code byte c. Measured on
-// MI355X with uniform random bytes, a wave64 ds_read_b128 costs about 12 CU cycles against 6.4 for b32, so
-// QG = 4 gives ~2.1x the lookups per cycle of one table per query. NG groups share every code load.
+// LDS tables. A group of QG queries shares one table laid out [s][c][QG] entries, so a single ds_read_b32 /
+// b64 / b128 at ((s * 256 + c) * QG * entry bytes) returns the entries of all QG queries for code byte c.
+// Measured on MI355X with uniform random bytes, a wave64 ds_read_b128 costs about 12 CU cycles against 6.4 for
+// b32, so 16-byte entry groups give ~2.1x the lookups per cycle of one fp32 table per query. NG groups share
+// every code load. fp16 tables put 8 queries in one 16-byte read.
 //
-// Exactness. Each query's distance is summed in sub-space order s = 0..m-1 from 0.f, exactly like the CPU
-// reference (cpu_ref.cpp:46-49), so GPU and CPU distances are bit-identical and ids agree exactly under the
-// (dist, id) order.
+// Exactness. Each query's distance is summed in fp32 in sub-space order s = 0..m-1 from 0.f, exactly like the
+// CPU reference (cpu_ref.cpp:46-49), so fp32-table distances are bit-identical to the CPU's and ids agree exactly
+// under the (dist, id) order. fp16 tables hold each query's fp32 entries scaled by a power of two (so that the
+// largest lies in [2^14, 2^15)) and rounded to nearest-even binary16; the sums stay fp32 and are scaled back
+// exactly, which the CPU restatement of the fp16 path reproduces bit for bit.
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.hpp"
 
 namespace vk {
 
-template <int QG>
-struct LdsVec;
-template <>
-struct LdsVec<1> {
-    using T = float;
-    __device__ static void add(float* acc, float v) { acc[0] += v; }
-};
-template <>
-struct LdsVec<2> {
-    using T = float2;
-    __device__ static void add(float* acc, float2 v) {
-        acc[0] += v.x;
-        acc[1] += v.y;
+// acc + (binary16 in the low / high half of h2) as fma(widened half, one, acc) with `one` a binary16 1.0 the
+// compiler cannot see through (opaque_half_one): the product is exact, so the single rounding equals an fp32 add of
+// the widened value, and the backend selects one v_fma_mix_f32 (op_sel picks the half) instead of a conversion and
+// an add. A literal 1.0 would be folded into an fadd, which has no mixed-precision form.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float add_half_lo(float acc, uint32_t h2, _Float16 one) {
+    return __builtin_fmaf(static_cast<float>(__builtin_bit_cast(half2_t, h2).x), static_cast<float>(one), acc);
+}
+__device__ __forceinline__ float add_half_hi(float acc, uint32_t h2, _Float16 one) {
+    return __builtin_fmaf(static_cast<float>(__builtin_bit_cast(half2_t, h2).y), static_cast<float>(one), acc);
+}
+__device__ __forceinline__ _Float16 opaque_half_one() {
+    uint32_t bits = 0x3c00u;  // binary16 1.0
+    asm volatile("" : "+s"(bits));
+    return __builtin_bit_cast(_Float16, static_cast<uint16_t>(bits));
+}
+
+// One LDS read of a table entry group: QG consecutive fp32 or fp16 entries.
+template <int QG, bool F16>
+struct Entries {
+    static constexpr int kBytes = (F16 ? 2 : 4) * QG;
+    using T = std::conditional_t<
+        F16,
+        std::conditional_t<QG == 1, uint16_t,
+                           std::conditional_t<QG == 2, uint32_t, std::conditional_t<QG == 4, uint2, uint4>>>,
+        std::conditional_t<QG == 1, float, std::conditional_t<QG == 2, float2, float4>>>;
+    __device__ static void add(float* acc, const T& v, _Float16 one) {
+        if constexpr (!F16) {
+            if constexpr (QG == 1) {
+                acc[0] += v;
+            } else if constexpr (QG == 2) {
+                acc[0] += v.x;
+                acc[1] += v.y;
+            } else {
+                acc[0] += v.x;
+                acc[1] += v.y;
+                acc[2] += v.z;
+                acc[3] += v.w;
+            }
+        } else {
+            if constexpr (QG == 1) {
+                acc[0] = add_half_lo(acc[0], static_cast<uint32_t>(v), one);
+            } else if constexpr (QG == 2) {
+                acc[0] = add_half_lo(acc[0], v, one);
+                acc[1] = add_half_hi(acc[1], v, one);
+            } else if constexpr (QG == 4) {
+                acc[0] = add_half_lo(acc[0], v.x, one);
+                acc[1] = add_half_hi(acc[1], v.x, one);
+                acc[2] = add_half_lo(acc[2], v.y, one);
+                acc[3] = add_half_hi(acc[3], v.y, one);
+            } else {
+                acc[0] = add_half_lo(acc[0], v.x, one);
+                acc[1] = add_half_hi(acc[1], v.x, one);
+                acc[2] = add_half_lo(acc[2], v.y, one);
+                acc[3] = add_half_hi(acc[3], v.y, one);
+                acc[4] = add_half_lo(acc[4], v.z, one);
+                acc[5] = add_half_hi(acc[5], v.z, one);
+                acc[6] = add_half_lo(acc[6], v.w, one);
+                acc[7] = add_half_hi(acc[7], v.w, one);
+            }
+        }
     }
 };
-template <>
-struct LdsVec<4> {
-    using T = float4;
-    __device__ static void add(float* acc, float4 v) {
-        acc[0] += v.x;
-        acc[1] += v.y;
-        acc[2] += v.z;
-        acc[3] += v.w;
-    }
-};
+
+// Power-of-two exponent applied to one query's fp16 table: the largest fp32 entry (as raw bits; entries are
+// >= 0) is brought into [2^14, 2^15), well inside binary16's range. 0 for an all-zero, infinite or NaN table.
+__device__ __forceinline__ int table_shift(uint32_t max_bits) {
+    if (max_bits == 0u || max_bits >= 0x7f800000u) return 0;
+    const int e = max_bits >= 0x00800000u ? static_cast<int>(max_bits >> 23) - 127
+                                          : -126 - (static_cast<int>(__clz(max_bits)) - 8);
+    return e - 14;
+}
+
+__device__ __forceinline__ uint32_t to_half_bits(float x) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
 
 // Loads n consecutive floats from p (16-byte aligned when n % 4 == 0, 8-byte aligned when n == 2) with the widest
 // vector loads the alignment allows.
@@ -74,34 +130,22 @@ __device__ __forceinline__ void load_floats(const float* p, float* out) {
     }
 }
 
-// Builds the NG query-interleaved tables of a slab in LDS: entry (s, c) of query q is
-// sum_j (x_q[s*dsub + j] - C[s][c][j])^2 with j in order and a separate multiply and add, the CPU reference's
-// arithmetic (cpu_ref.cpp:7-14, common.hpp:27-34). Wave w takes sub-spaces w, w + W, ..., so the query values it
-// reads are wave-uniform (scalar loads); lane l takes centroids l, l + 64, l + 128, l + 192. With the sub-vector
-// width DSUB known at compile time, the four centroids' loads of a sub-space are issued together, so a build costs
-// about one memory round trip per sub-space a wave handles rather than one per element. DSUB = 0: any width.
-// Padded query slots read the last real query; their entries are never used.
-template <int QG, int NG, int M, int W, int DSUB>
-__device__ __forceinline__ void build_tables_w(const WaveScanArgs& a, int64_t slab, float* lds, int wave, int lane) {
+// Computes the fp32 table entries of a slab's QS queries and hands each (s, c) to sink(s, c, acc[QS]): entry (s, c)
+// of query q is sum_j (x_q[s*dsub + j] - C[s][c][j])^2 with j in order and a separate multiply and add, the CPU
+// reference's arithmetic (cpu_ref.cpp:7-14, common.hpp:27-34). Wave w takes sub-spaces w, w + W, ..., so the query
+// values it reads are wave-uniform (scalar loads); lane l takes centroids l, l + 64, l + 128, l + 192. With the
+// sub-vector width DSUB known at compile time, the four centroids' loads of a sub-space are issued together, so a
+// pass costs about one memory round trip per sub-space a wave handles rather than one per element. DSUB = 0: any
+// width. Padded query slots read the last real query; their entries are never used.
+template <int QS, int M, int W, int DSUB, typename Sink>
+__device__ __forceinline__ void table_entries_w(const WaveScanArgs& a, int64_t slab, int wave, int lane, Sink& sink) {
 #pragma clang fp contract(off)
-    constexpr int QS = QG * NG;
     constexpr int R = KSUB / WAVE;  // centroids per lane and sub-space
     const int m = M ? M : a.m;
     const int dsub = DSUB ? DSUB : a.d / m;
-    const int table = m * KSUB * QG;
     const float* qrow[QS];
 #pragma unroll
     for (int q = 0; q < QS; ++q) qrow[q] = a.queries + std::min<int64_t>(slab * QS + q, a.nq - 1) * a.d;
-    auto store = [&](int s, int c, const float* acc) {
-#pragma unroll
-        for (int t = 0; t < NG; ++t) {
-            float* dst = lds + t * table + (s * KSUB + c) * QG;
-            if constexpr (QG == 4) *reinterpret_cast<float4*>(dst) = make_float4(acc[t * 4], acc[t * 4 + 1],
-                                                                                 acc[t * 4 + 2], acc[t * 4 + 3]);
-            else if constexpr (QG == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc[t * 2], acc[t * 2 + 1]);
-            else dst[0] = acc[t];
-        }
-    };
     for (int s = wave; s < m; s += W) {
         const float* cbase = a.centroids + static_cast<int64_t>(s) * KSUB * dsub;
         if constexpr (DSUB > 0) {
@@ -125,7 +169,7 @@ __device__ __forceinline__ void build_tables_w(const WaveScanArgs& a, int64_t sl
                         acc[q] += diff * diff;
                     }
                 }
-                store(s, r * WAVE + lane, acc);
+                sink(s, r * WAVE + lane, acc);
             }
         } else {
             for (int r = 0; r < R; ++r) {
@@ -142,20 +186,92 @@ __device__ __forceinline__ void build_tables_w(const WaveScanArgs& a, int64_t sl
                         acc[q] += diff * diff;
                     }
                 }
-                store(s, c, acc);
+                sink(s, c, acc);
             }
         }
     }
 }
 
-// Sub-vector widths of d = 128 at m = 16, 32, 64 (and 64 at m = 16) get an unrolled build; others the generic one.
-template <int QG, int NG, int M, int W>
-__device__ __forceinline__ void build_tables(const WaveScanArgs& a, int64_t slab, float* lds, int wave, int lane) {
+// Sub-vector widths of d = 128 at m = 16, 32, 64 (and 64 at m = 16) get an unrolled pass; others the generic one.
+template <int QS, int M, int W, typename Sink>
+__device__ __forceinline__ void table_entries(const WaveScanArgs& a, int64_t slab, int wave, int lane, Sink& sink) {
     const int dsub = a.d / (M ? M : a.m);
-    if (dsub == 8) build_tables_w<QG, NG, M, W, 8>(a, slab, lds, wave, lane);
-    else if (dsub == 4) build_tables_w<QG, NG, M, W, 4>(a, slab, lds, wave, lane);
-    else if (dsub == 2) build_tables_w<QG, NG, M, W, 2>(a, slab, lds, wave, lane);
-    else build_tables_w<QG, NG, M, W, 0>(a, slab, lds, wave, lane);
+    if (dsub == 8) table_entries_w<QS, M, W, 8>(a, slab, wave, lane, sink);
+    else if (dsub == 4) table_entries_w<QS, M, W, 4>(a, slab, wave, lane, sink);
+    else if (dsub == 2) table_entries_w<QS, M, W, 2>(a, slab, wave, lane, sink);
+    else table_entries_w<QS, M, W, 0>(a, slab, wave, lane, sink);
+}
+
+// Writes the NG query-interleaved tables of a slab into LDS (`tables`, NG tables of table_bytes each). fp16 tables
+// take each query's power-of-two shift from the per-query maxima in `qmax` (raw fp32 bits).
+template <int QG, int NG, int M, int W, bool F16>
+__device__ __forceinline__ void build_tables(const WaveScanArgs& a, int64_t slab, unsigned char* tables,
+                                             int table_bytes, const unsigned* qmax, int wave, int lane) {
+    constexpr int QS = QG * NG;
+    constexpr int EB = Entries<QG, F16>::kBytes;
+    if constexpr (!F16) {
+        auto sink = [&](int s, int c, const float* acc) {
+#pragma unroll
+            for (int t = 0; t < NG; ++t) {
+                unsigned char* dst = tables + t * table_bytes + (s * KSUB + c) * EB;
+                if constexpr (QG == 4) *reinterpret_cast<float4*>(dst) = make_float4(acc[t * 4], acc[t * 4 + 1],
+                                                                                     acc[t * 4 + 2], acc[t * 4 + 3]);
+                else if constexpr (QG == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc[t * 2], acc[t * 2 + 1]);
+                else *reinterpret_cast<float*>(dst) = acc[t];
+            }
+        };
+        table_entries<QS, M, W>(a, slab, wave, lane, sink);
+    } else {
+        int shift[QS];
+#pragma unroll
+        for (int q = 0; q < QS; ++q) shift[q] = table_shift(qmax[q]);
+        auto sink = [&](int s, int c, const float* acc) {
+            uint32_t h[QS];
+#pragma unroll
+            for (int q = 0; q < QS; ++q) h[q] = to_half_bits(ldexpf(acc[q], -shift[q]));
+#pragma unroll
+            for (int t = 0; t < NG; ++t) {
+                unsigned char* dst = tables + t * table_bytes + (s * KSUB + c) * EB;
+                const uint32_t* g = h + t * QG;
+                if constexpr (QG == 8)
+                    *reinterpret_cast<uint4*>(dst) = make_uint4(g[0] | g[1] << 16, g[2] | g[3] << 16,
+                                                                g[4] | g[5] << 16, g[6] | g[7] << 16);
+                else if constexpr (QG == 4)
+                    *reinterpret_cast<uint2*>(dst) = make_uint2(g[0] | g[1] << 16, g[2] | g[3] << 16);
+                else if constexpr (QG == 2) *reinterpret_cast<uint32_t*>(dst) = g[0] | g[1] << 16;
+                else *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(g[0]);
+            }
+        };
+        table_entries<QS, M, W>(a, slab, wave, lane, sink);
+    }
+}
+
+// Per-query maximum of a slab's fp32 table entries, as raw bits (entries are >= 0, so the unsigned order is the
+// float order, with NaN above +inf): lane maxima, a wave reduction, one LDS atomicMax per (wave, query). qmax must
+// be zero beforehand; the caller synchronises after.
+template <int QS, int M, int W>
+__device__ __forceinline__ void table_maxima(const WaveScanArgs& a, int64_t slab, unsigned* qmax, int wave, int lane) {
+    uint32_t mx[QS];
+#pragma unroll
+    for (int q = 0; q < QS; ++q) mx[q] = 0u;
+    auto sink = [&](int, int, const float* acc) {
+#pragma unroll
+        for (int q = 0; q < QS; ++q) mx[q] = max(mx[q], __float_as_uint(acc[q]));
+    };
+    table_entries<QS, M, W>(a, slab, wave, lane, sink);
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+#pragma unroll
+        for (int o = WAVE / 2; o > 0; o >>= 1)
+            mx[q] = max(mx[q], static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx[q]), o)));
+        if (lane == 0) atomicMax(qmax + q, mx[q]);
+    }
+}
+
+// The value a final result carries: fp16-table sums are scaled back by the table's power of two (exact).
+__device__ __forceinline__ Pair final_pair(float d, int32_t id, int shift) {
+    if (id == kEmptyId) return Pair{INFINITY, -1};
+    return Pair{shift ? ldexpf(d, shift) : d, id};
 }
 
 // Streams pairs [begin, all) of consecutive partial lists through a wave list: four 64-pair chunks per round (four
@@ -177,72 +293,76 @@ __device__ __forceinline__ void stream_pairs(WaveList<S>& wl, const Pair* first,
 }
 
 // Final merge of one query of a slab by a single wave (few partial lists): no barriers; the wave list's first k
-// entries are the results, empty slots written as the reference's {+inf, -1}.
+// entries are the results.
 template <int S>
-__device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, int K, int k, Pair* out, int lane) {
+__device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, int K, int k, Pair* out, int shift,
+                                                 int lane) {
     WaveList<S> wl;
     wl.init();
     stream_pairs(wl, first, 0, 4 * WAVE, lists * K, K, lane);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int j = s * WAVE + lane;
-        if (j < k) out[j] = wl.id[s] == kEmptyId ? Pair{INFINITY, -1} : Pair{wl.d[s], wl.id[s]};
+        if (j < k) out[j] = final_pair(wl.d[s], wl.id[s], shift);
     }
 }
 
 // Final merge of one query of a slab by the last block to finish the slab: the slab's `lists` partial lists for
 // the query (K pairs each, `first[l * K + j]`) are split over the W waves, each streaming its share through a wave
-// list, four 64-pair chunks per round; the W wave lists are then merged by rank into the query's k results. LDS
-// `buf` holds W * K pairs. Called by all threads of the block.
+// list; the W wave lists are then merged by rank into the query's k results. LDS `buf` holds W * K pairs. Called
+// by all threads of the block.
 template <int S, int W>
-__device__ __forceinline__ void merge_query(const Pair* first, int lists, int K, int k, Pair* out, Pair* buf,
-                                            int tid, int wave, int lane) {
+__device__ __forceinline__ void merge_query(const Pair* first, int lists, int K, int k, Pair* out, int shift,
+                                            Pair* buf, int tid, int wave, int lane) {
     WaveList<S> wl;
     wl.init();
     stream_pairs(wl, first, wave * 4 * WAVE, W * 4 * WAVE, lists * K, K, lane);
     wl.store(buf + wave * K, K);
     __syncthreads();
-    merge_lists(buf, W, K, out, tid, W * WAVE, k, true);
+    merge_lists(buf, W, K, out, tid, W * WAVE, k, true, shift);
     __syncthreads();
 }
 
-// QG: queries per table (1, 2, 4). NG: tables per block (1, 2). U: 64-vector tiles per wave step.
-// M: sub-spaces if fixed at compile time, 0 for any m % 16 == 0. S: list registers per lane (K <= 64 * S).
-// Waves per SIMD the block residency allows: blocks per CU are bounded by LDS (tables of QG*NG*M KB) and by
-// 2048 threads; the register budget is set so that residency is not cut further by VGPRs (4 waves -> 128).
-template <int QG, int NG, int M, int T>
+// QG: queries per table (1, 2, 4; 8 with fp16 entries). NG: tables per block (1, 2). U: 64-vector tiles per wave
+// step. M: sub-spaces if fixed at compile time, 0 for any m % 16 == 0. S: list registers per lane (K <= 64 * S).
+// F16: binary16 table entries.
+// Waves per SIMD the block residency allows: blocks per CU are bounded by LDS (the NG tables) and by 2048
+// threads; the register budget is set so that residency is not cut further by VGPRs (4 waves -> 128).
+template <int QG, int NG, int M, int T, bool F16>
 constexpr int wave_kernel_waves_per_simd() {
     if (M == 0) return 1;
-    const int by_lds = (160 * 1024) / (QG * NG * (M ? M : 16) * KSUB * 4);
+    const int by_lds = (160 * 1024) / (NG * (M ? M : 16) * KSUB * Entries<QG, F16>::kBytes);
     const int blocks = by_lds < 2048 / T ? by_lds : 2048 / T;
     const int waves = blocks * (T / WAVE) / 4;
     return waves < 1 ? 1 : (waves > 4 ? 4 : waves);
 }
 
-template <int QG, int NG, int U, int M, int S, int T>
+template <int QG, int NG, int U, int M, int S, int T, bool F16>
 __global__ void __launch_bounds__(T)
-    __attribute__((amdgpu_waves_per_eu(wave_kernel_waves_per_simd<QG, NG, M, T>())))
+    __attribute__((amdgpu_waves_per_eu(wave_kernel_waves_per_simd<QG, NG, M, T, F16>())))
     fused_wave_kernel_t(WaveScanArgs a) {
     constexpr int QS = QG * NG;
     constexpr int W = T / WAVE;
-    using V = typename LdsVec<QG>::T;
+    using E = Entries<QG, F16>;
+    using V = typename E::T;
     // With m fixed the tables are a static LDS array at address 0, so a lookup address is one SDWA shift of
     // the code byte plus a compile-time immediate offset; a dynamic (extern) array's base is a link-time
     // symbol that costs two more VALU adds per lookup.
-    constexpr int kStaticFloats = M ? QG * NG * M * KSUB : 4;
-    __shared__ __align__(16) float lds_static[kStaticFloats];
-    extern __shared__ __align__(16) float lds_dynamic[];
+    constexpr int kStaticVec = M ? NG * M * KSUB * E::kBytes / 16 : 1;
+    __shared__ uint4 lds_static[kStaticVec];
+    extern __shared__ uint4 lds_dynamic[];
     __shared__ bool last_block;
-    float* const lds_base = M ? lds_static : lds_dynamic;
-    const float* lds = lds_base;
+    __shared__ unsigned qmax[QS];  // fp16 tables: per-query maximum entry of the current slab (raw bits)
+    unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
     const int words = m / 16;
-    const int table = m * KSUB * QG;  // floats per group table
+    const int table_bytes = m * KSUB * E::kBytes;  // one group table
     // The wave index is the same in every lane; reading it through a scalar register lets the compiler keep the
     // granule, tile and id arithmetic of the scan loop on the scalar unit.
     const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int64_t grid = gridDim.x, b = blockIdx.x;
     const int64_t start = b * a.total / grid, end = (b + 1) * a.total / grid;
+    const _Float16 one = opaque_half_one();
 
     for (int64_t item = start; item < end;) {
         const int64_t slab = item / a.n_gran;
@@ -250,7 +370,13 @@ __global__ void __launch_bounds__(T)
         const int64_t g_hi = min(end - slab * a.n_gran, a.n_gran);
 
         __syncthreads();  // the previous slab's merge has finished with LDS
-        build_tables<QG, NG, M, W>(a, slab, lds_base, wave, lane);
+        if constexpr (F16) {
+            if (tid < QS) qmax[tid] = 0u;
+            __syncthreads();
+            table_maxima<QS, M, W>(a, slab, qmax, wave, lane);
+            __syncthreads();
+        }
+        build_tables<QG, NG, M, W, F16>(a, slab, tables, table_bytes, qmax, wave, lane);
         __syncthreads();
 
         // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so the
@@ -293,8 +419,9 @@ __global__ void __launch_bounds__(T)
                         const int s = w * 16 + j;
 #pragma unroll
                         for (int t = 0; t < NG; ++t) {
-                            const V v = *reinterpret_cast<const V*>(lds + t * table + (s * KSUB + (int)c) * QG);
-                            LdsVec<QG>::add(&acc[t * QG], v);
+                            const V v = *reinterpret_cast<const V*>(tables + t * table_bytes +
+                                                                    (s * KSUB + static_cast<int>(c)) * E::kBytes);
+                            E::add(&acc[t * QG], v, one);
                         }
                     }
                 };
@@ -320,7 +447,7 @@ __global__ void __launch_bounds__(T)
         const int slot = static_cast<int>(b - first_block_of(slab * a.n_gran, grid, a.total));
         const int lpb = a.lists_per_block;
         Pair* const slab_part = a.part + slab * QS * a.max_slots * lpb * static_cast<int64_t>(a.K);
-        Pair* const buf = reinterpret_cast<Pair*>(lds_base);  // QS * W * K pairs fit in the tables' space
+        Pair* const buf = reinterpret_cast<Pair*>(tables);  // QS * W * K pairs fit in the tables' space
         if (lpb == 1) {
             __syncthreads();  // every wave has finished reading the tables
 #pragma unroll
@@ -352,57 +479,66 @@ __global__ void __launch_bounds__(T)
             if (lpb == W) {  // at most 8 blocks per slab: one wave per query
                 for (int q = wave; q < QS && slab * QS + q < a.nq; q += W)
                     merge_query_wave<S>(slab_part + q * a.max_slots * W * a.K, count * W, a.K, a.k,
-                                        a.out + (slab * QS + q) * a.k, lane);
+                                        a.out + (slab * QS + q) * a.k, F16 ? table_shift(qmax[q]) : 0, lane);
             } else {
                 for (int q = 0; q < QS && slab * QS + q < a.nq; ++q)
                     merge_query<S, W>(slab_part + q * a.max_slots * a.K, count, a.K, a.k,
-                                      a.out + (slab * QS + q) * a.k, buf, tid, wave, lane);
+                                      a.out + (slab * QS + q) * a.k, F16 ? table_shift(qmax[q]) : 0, buf, tid,
+                                      wave, lane);
             }
         }
         item = (slab + 1) * a.n_gran;
     }
 }
 
-template <int QG, int NG, int U, int M, int S, int T>
+template <int QG, int NG, int U, int M, int S, int T, bool F16>
 hipError_t launch_fused_wave_t(const WaveScanArgs& a, int grid, size_t smem, hipStream_t stream) {
-    hipLaunchKernelGGL((fused_wave_kernel_t<QG, NG, U, M, S, T>), dim3(grid), dim3(T), smem, stream, a);
+    hipLaunchKernelGGL((fused_wave_kernel_t<QG, NG, U, M, S, T, F16>), dim3(grid), dim3(T), smem, stream, a);
     return hipGetLastError();
 }
 
-template <int QG, int NG, int U, int M, int S>
+template <int QG, int NG, int U, int M, int S, bool F16>
 WaveScanKernel make_wave_kernel() {
     constexpr int T = 512;
     WaveScanKernel k;
-    k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T>);
+    k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T, F16>);
     k.threads = T;
     k.dynamic_lds = M == 0;
-    k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T>;
+    k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T, F16>;
     return k;
 }
 
-// Instances for one M: every (QG, NG) whose tables fit in 160 KB of LDS when M is known.
-template <int M>
+// Instances for one M and entry type: every (QG, NG) whose tables fit in 160 KB of LDS when M is known. fp32
+// tables: QG 1, 2, 4 and two groups of 4; fp16 tables: QG 1, 2, 4, 8 in one group.
+template <int M, bool F16>
 WaveScanKernel select_wave_kernel(int qg, int ng, int ilp, int segments) {
     constexpr int kLds = 160 * 1024;
 #define VK_WAVE_CASE(QG_, NG_)                                                                      \
     if (qg == QG_ && ng == NG_) {                                                                   \
-        if constexpr (M == 0 || QG_ * NG_ * M * KSUB * 4 <= kLds) {                                 \
+        if constexpr (M == 0 || NG_ * M * KSUB * Entries<QG_, F16>::kBytes <= kLds) {               \
             if (segments == 1) {                                                                    \
-                if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 1>();                         \
-                if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 1>();                         \
-                if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 1>();                         \
+                if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 1, F16>();                    \
+                if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 1, F16>();                    \
+                if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 1, F16>();                    \
             } else if (segments == 2) {                                                             \
-                if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 2>();                         \
-                if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 2>();                         \
-                if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 2>();                         \
+                if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 2, F16>();                    \
+                if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 2, F16>();                    \
+                if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 2, F16>();                    \
             }                                                                                       \
         }                                                                                           \
         return WaveScanKernel{};                                                                    \
     }
-    VK_WAVE_CASE(1, 1)
-    VK_WAVE_CASE(2, 1)
-    VK_WAVE_CASE(4, 1)
-    VK_WAVE_CASE(4, 2)
+    if constexpr (!F16) {
+        VK_WAVE_CASE(1, 1)
+        VK_WAVE_CASE(2, 1)
+        VK_WAVE_CASE(4, 1)
+        VK_WAVE_CASE(4, 2)
+    } else {
+        VK_WAVE_CASE(1, 1)
+        VK_WAVE_CASE(2, 1)
+        VK_WAVE_CASE(4, 1)
+        VK_WAVE_CASE(8, 1)
+    }
 #undef VK_WAVE_CASE
     return WaveScanKernel{};
 }

@@ -1,0 +1,8 @@
+// Instances of the fused wave-list scan with fp16 tables for m = 64.
+#include "fused_wave.inl"
+
+namespace vk {
+WaveScanKernel fused_wave_kernel_h64(int qg, int ng, int ilp, int segments) {
+    return select_wave_kernel<64, true>(qg, ng, ilp, segments);
+}
+}  // namespace vk

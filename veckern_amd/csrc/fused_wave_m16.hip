@@ -3,6 +3,6 @@
 
 namespace vk {
 WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments) {
-    return select_wave_kernel<16>(qg, ng, ilp, segments);
+    return select_wave_kernel<16, false>(qg, ng, ilp, segments);
 }
 }  // namespace vk

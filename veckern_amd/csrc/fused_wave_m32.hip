@@ -3,6 +3,6 @@
 
 namespace vk {
 WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments) {
-    return select_wave_kernel<32>(qg, ng, ilp, segments);
+    return select_wave_kernel<32, false>(qg, ng, ilp, segments);
 }
 }  // namespace vk

@@ -3,6 +3,6 @@
 
 namespace vk {
 WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments) {
-    return select_wave_kernel<0>(qg, ng, ilp, segments);
+    return select_wave_kernel<0, false>(qg, ng, ilp, segments);
 }
 }  // namespace vk

@@ -197,12 +197,13 @@ int main(int argc, char** argv) try {
 
     std::vector<Row> rows;
     using gpu::ScanVariant;
-    for (int vi = 0; vi <= static_cast<int>(ScanVariant::FusedWarp); ++vi) {
+    for (int vi = 0; vi <= static_cast<int>(ScanVariant::FusedWarpF16); ++vi) {
         const auto v = static_cast<ScanVariant>(vi);
         const std::string name = gpu::variant_name(v);
         if (!wanted(o.variants, name)) continue;
         const bool needs16 = v == ScanVariant::SharedLutVec || v == ScanVariant::FusedVec ||
-                             v == ScanVariant::FusedVecMQ || v == ScanVariant::FusedWarp;
+                             v == ScanVariant::FusedVecMQ || v == ScanVariant::FusedWarp ||
+                             v == ScanVariant::FusedWarpF16;
         if (needs16 && o.m % 16 != 0) continue;
         if (v == ScanVariant::Fused) {
             std::printf("%s: not launched in this build (its scratch-resident per-thread list faulted the GPU); "

@@ -27,6 +27,7 @@ Timings from_c(const vk_timings& t) { return Timings{t.transfer_ms, t.lut_ms, t.
 
 static_assert(sizeof(Neighbor) == sizeof(vk_neighbor), "Neighbor and vk_neighbor must share a layout");
 static_assert(static_cast<int>(ScanVariant::FusedWarp) == VK_V8_FUSED_WARP, "variant numbering");
+static_assert(static_cast<int>(ScanVariant::FusedWarpF16) == VK_V9_FUSED_WARP_F16, "variant numbering");
 
 }  // namespace
 

@@ -49,8 +49,8 @@ struct WaveScanKernel {
     hipError_t (*launch)(const WaveScanArgs&, int grid, size_t smem, hipStream_t) = nullptr;
 };
 
-// Returns a kernel with fn == nullptr when the combination is not built.
-WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments);
+// Returns a kernel with fn == nullptr when the combination is not built. f16: binary16 tables (v9).
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16);
 
 // Blocks covering slab `slab` in the balanced partition of `total` work items over `grid` blocks
 // (block b owns items [b*total/grid, (b+1)*total/grid)).

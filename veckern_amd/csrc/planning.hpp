@@ -17,14 +17,22 @@ inline int dispatched_k(size_t k) {
 
 // v3-v5 read the byte-interleaved layout, v6-v8 the 16-byte-word one (searcher.cu:222-241).
 inline bool uses_byte_layout(int v) { return v == 3 || v == 4 || v == 5; }
-inline bool uses_word_layout(int v) { return v == 6 || v == 7 || v == 8; }
+inline bool uses_word_layout(int v) { return v == 6 || v == 7 || v == 8 || v == 9; }
 
-// Queries per block: the requested Q, halved until the Q tables (Q * m KB) fit in LDS; for per-thread lists
-// (v7) also until Q * K <= 64, as searcher.cu:213-220.
-inline int effective_q(int requested, size_t m, size_t max_lds, bool per_thread_lists, int K) {
+// Queries per block: the requested Q, halved until the Q tables (Q * m * 256 entries) fit in LDS; for per-thread
+// lists (v7) also until Q * K <= 64, as searcher.cu:213-220. entry_bytes: 4 for fp32 tables, 2 for fp16.
+inline int effective_q(int requested, size_t m, size_t max_lds, bool per_thread_lists, int K,
+                       size_t entry_bytes = sizeof(float)) {
     int q = std::max(requested, 1);
-    while (q > 1 && ((per_thread_lists && q * K > 64) || static_cast<size_t>(q) * m * 256 * sizeof(float) > max_lds))
+    while (q > 1 && ((per_thread_lists && q * K > 64) || static_cast<size_t>(q) * m * 256 * entry_bytes > max_lds))
         q /= 2;
+    return q;
+}
+
+// A slab never holds more query slots than the batch needs: Q is halved while half of it still covers nq
+// (nq = 1 scans with one table per block, whose b32 reads cost half the LDS time of a 4-query b128 read).
+inline int cap_q_by_batch(int q, size_t nq) {
+    while (q > 1 && static_cast<size_t>(q / 2) >= nq) q /= 2;
     return q;
 }
 
