@@ -42,12 +42,18 @@ __device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgc
 // One sorted list of up to 64*S (dist, id) pairs spread over a wave: entry p lives in lane p % 64, register
 // p / 64. The admission threshold (entry K-1) is wave-uniform, so the compiler keeps it in SGPRs. Every
 // member must be called by all 64 lanes with wave-uniform arguments (control flow stays uniform).
+//
+// `cap` is an optional outside bound: the threshold of another list over a disjoint part of the same candidate
+// stream (a sibling wave's). A candidate farther than it has K better candidates in that list, so it cannot be in
+// the merged top K and is not offered; ties at the cap are still offered, which keeps the (dist, id) order exact.
 template <int S>
 struct WaveList {
     float d[S];
     int32_t id[S];
     float thr_d;
     int32_t thr_i;
+    float cap;     // outside bound, +inf when none
+    float filter;  // min(thr_d, cap): the ballot pre-test of offers
 
     __device__ __forceinline__ void init() {
 #pragma unroll
@@ -57,6 +63,19 @@ struct WaveList {
         }
         thr_d = INFINITY;
         thr_i = kEmptyId;
+        cap = INFINITY;
+        filter = INFINITY;
+    }
+
+    // A list that must admit nothing (a padded query slot).
+    __device__ __forceinline__ void disable() {
+        thr_d = -INFINITY;
+        filter = -INFINITY;
+    }
+
+    __device__ __forceinline__ void set_cap(float c) {
+        cap = c;
+        filter = fminf(thr_d, cap);
     }
 
     // Inserts the wave-uniform pair (x, xi) at its sorted position; entries behind it move one place back.
@@ -106,6 +125,7 @@ struct WaveList {
             thr_d = lane_read(d[S - 1], t - (S - 1) * WAVE);
             thr_i = lane_read(id[S - 1], t - (S - 1) * WAVE);
         }
+        filter = fminf(thr_d, cap);
     }
 
     // Each lane offers one candidate; admitted ones are inserted one at a time, lowest lane first. The ballot
@@ -118,7 +138,7 @@ struct WaveList {
     // As offer, with the lanes that hold candidates given as a wave-uniform mask: the common no-candidate case is
     // one compare into a scalar mask and one branch.
     __device__ __forceinline__ void offer_masked(float x, int32_t xi, uint64_t valid, int K) {
-        uint64_t mask = __builtin_amdgcn_ballot_w64(x <= thr_d) & valid;
+        uint64_t mask = __builtin_amdgcn_ballot_w64(x <= filter) & valid;
         while (mask) {
             const int src = __ffsll(static_cast<unsigned long long>(mask)) - 1;
             mask &= mask - 1;

@@ -353,6 +353,9 @@ __global__ void __launch_bounds__(T)
     extern __shared__ uint4 lds_dynamic[];
     __shared__ bool last_block;
     __shared__ unsigned qmax[QS];  // fp16 tables: per-query maximum entry of the current slab (raw bits)
+    // Per query, the lowest list threshold any wave of the block has published for the current slab (raw bits of
+    // a distance >= 0, so unsigned order is float order): every wave filters its offers by it.
+    __shared__ __align__(16) unsigned bound[QS];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
     const int words = m / 16;
@@ -377,6 +380,7 @@ __global__ void __launch_bounds__(T)
             __syncthreads();
         }
         build_tables<QG, NG, M, W, F16>(a, slab, tables, table_bytes, qmax, wave, lane);
+        if (tid < QS) bound[tid] = 0x7f800000u;  // +inf
         __syncthreads();
 
         // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so the
@@ -386,11 +390,14 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
         for (int q = 0; q < QS; ++q) {
             lists[q].init();
-            if (q >= live) lists[q].thr_d = -INFINITY;
+            if (q >= live) lists[q].disable();
         }
         const uint32_t n32 = static_cast<uint32_t>(a.n);  // n < 2^31: ids and tile bounds fit in 32 bits
 
         for (int64_t g = g_lo + wave; g < g_hi; g += W) {
+            // The block's best published thresholds (a stale value is only a looser bound).
+#pragma unroll
+            for (int q = 0; q < QS; ++q) lists[q].set_cap(__uint_as_float(bound[q]));
             const int64_t tile0 = g * U;
             const uint4* tile_codes = a.codes + tile0 * words * WAVE + lane;  // wave-uniform base + lane
             // All code words of the U tiles are loaded first (the global-load ILP). The lookups then run one
@@ -439,6 +446,10 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
                 for (int q = 0; q < QS; ++q) lists[q].offer_masked(acc[q], static_cast<int32_t>(id), valid, a.K);
             }
+            // Publish thresholds that beat the block's bound (lists fill and tighten independently per wave).
+#pragma unroll
+            for (int q = 0; q < QS; ++q)
+                if (lists[q].thr_d < lists[q].cap && lane == 0) atomicMin(bound + q, __float_as_uint(lists[q].thr_d));
         }
 
         // Partial lists of this (block, slab): part[slab][q][slot][list][K], the lists of one query contiguous.
