@@ -214,8 +214,9 @@ def main():
     q_eff = shape.queries_per_block
     hbm_bytes = float(n) * m * math.ceil(nq / q_eff)
     f16 = variant == vk.ScanVariant.FusedWarpF16
-    # fp16 tables: a read of 2*Q bytes serves Q queries, so the floor is twice the fp32 floor of the same read width
-    peak = (2 * floors[q_eff // 2] if q_eff >= 2 else floors[1]) if f16 else floors[best_qg]
+    # The floor of the table-read width the launch uses (fp32: Q entries per read, at most 16 bytes; fp16 tables: a
+    # read of 2*Q bytes serves Q queries, twice the fp32 floor of the same width). best_floor is the fastest width.
+    peak = (2 * floors[q_eff // 2] if q_eff >= 2 else floors[1]) if f16 else floors[min(q_eff, 4)]
     roofline = {
         "bound": "lds",
         "achieved": achieved / 1e12,
@@ -229,6 +230,7 @@ def main():
         "algorithmic": f"n*m*nq = {lookups:.3e} LDS lookups per launch (one {2 if f16 else 4}-byte table read + "
                        f"one fp32 add each)",
         "floor_by_table_width": {f"b{32 * q}_Q{q}": floors[q] / 1e12 for q in floors},
+        "best_floor": floors[best_qg] / 1e12,
         "hbm": {"achieved_gbs": hbm_bytes / (scan_ms * 1e-3) / 1e9, "peak_gbs": HBM_PEAK_GBS,
                 "frac": hbm_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "measured_read_gbs": hbm_gbs,
                 "algorithmic_bytes": hbm_bytes,
