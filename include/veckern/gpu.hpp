@@ -81,4 +81,23 @@ private:
     std::unique_ptr<Impl> impl_;
 };
 
+// Exact re-ranking on the GPU (not in the reference's gpu.hpp: its rerank_exact, cpu_ref.hpp:55-56, runs on the
+// CPU). The n x d base vectors are copied to the device once; rerank() takes the same arguments as rerank_exact
+// minus the base and returns bit-identical results (ids < 0 skipped; ids >= n throw std::invalid_argument).
+class Reranker {
+public:
+    Reranker(const float* base, std::size_t n, std::size_t d);
+    ~Reranker();
+    Reranker(const Reranker&) = delete;
+    Reranker& operator=(const Reranker&) = delete;
+
+    // candidates: nq x r; out: nq x k, ascending (dist, id), padded {+inf, -1}. 1 <= k <= 128.
+    Timings rerank(const float* queries, std::size_t nq, const Neighbor* candidates, std::size_t r, std::size_t k,
+                   Neighbor* out);
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
 }  // namespace veckern::gpu

@@ -93,6 +93,7 @@ typedef struct vk_device_info {
 } vk_device_info;
 
 typedef struct vk_searcher vk_searcher;
+typedef struct vk_reranker vk_reranker;
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* vk_last_error(void);
@@ -146,6 +147,23 @@ int vk_distances(vk_searcher* s, const float* queries, size_t nq, int variant, f
  * queries in and results out. */
 int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq, size_t k, int variant, vk_neighbor* d_out,
                      vk_timings* timings);
+
+/* Exact re-ranking on the GPU: replaces rerank_exact (cpu_ref.hpp:55-56, cpu_ref.cpp:66-77), the step after the
+ * search that bench --rerank R runs (bench_main.cpp:145-153). The reference re-ranks on the CPU from host arrays;
+ * here the n x d base vectors are copied to the current device once by vk_reranker_create, and each call scores
+ * the candidates of nq queries: for every candidate id in [0, n) the squared L2 distance summed in dimension order
+ * (bit-identical to the reference's l2sq), then the k smallest by (dist, id), padded {+inf, -1}. Candidate ids < 0
+ * are skipped, as in the reference; an id >= n is an error (VK_ERR_INVALID_ARGUMENT; the reference would read out
+ * of bounds) and that candidate is never read. k must be in [1, 128]. Timings: transfer_ms (host entry point)
+ * and scan_ms (the re-rank kernel). */
+int vk_reranker_create(const float* base, size_t n, size_t d, vk_reranker** out);
+void vk_reranker_destroy(vk_reranker* r);
+/* Host buffers: queries nq x d, candidates nq x r, out nq x k. */
+int vk_rerank(vk_reranker* r, const float* queries, size_t nq, const vk_neighbor* candidates, size_t r_per_query,
+              size_t k, vk_neighbor* out, vk_timings* timings);
+/* Device pointers on the re-ranker's device (for instance the output of vk_search_device). */
+int vk_rerank_device(vk_reranker* r, const float* d_queries, size_t nq, const vk_neighbor* d_candidates,
+                     size_t r_per_query, size_t k, vk_neighbor* d_out, vk_timings* timings);
 
 #ifdef __cplusplus
 }

@@ -42,6 +42,7 @@ def oracle() -> ctypes.CDLL:
         lib.vko_table_shift.restype = ctypes.c_int
         lib.vko_table_shift.argtypes = [_P, _S]
         lib.vko_adc_search_f16.argtypes = [_P, _S, _S, _P, _S, _P, _S, _S, _P]
+        lib.vko_rerank_exact.argtypes = [_P, _S, _P, _S, _P, _S, _S, _P]
         _oracle = lib
     return _oracle
 
@@ -66,6 +67,7 @@ def ref() -> ctypes.CDLL:
         lib.vkref_select_topk.argtypes = [_P, _S, _S, _S, _P]
         lib.vkref_adc_search.argtypes = [_P, _P, _S, _P, _S, _S, _P]
         lib.vkref_exact_knn.argtypes = [_P, _S, _P, _S, _S, _S, _P]
+        lib.vkref_rerank_exact.argtypes = [_P, _S, _P, _S, _P, _S, _S, _P]
         lib.vkref_recall_at_k.restype = ctypes.c_double
         lib.vkref_recall_at_k.argtypes = [_P, _S, _P, _S, _S, _S]
         lib.vkref_topk_run.argtypes = [_P, _P, _S, _S, _P]
@@ -130,6 +132,23 @@ def adc_search_f16(centroids: np.ndarray, d: int, codes: np.ndarray, queries: np
                                      out.ctypes.data)
     if rc != 0:
         raise ValueError("vko_adc_search_f16 rejected its input")
+    return out
+
+
+def rerank_exact(base: np.ndarray, queries: np.ndarray, candidates: np.ndarray, k: int,
+                 use_ref: bool = False) -> np.ndarray:
+    """Exact re-ranking of nq x r candidates (NEIGHBOR records; ids < 0 skipped) against base rows."""
+    base = _c(base, np.float32)
+    d = base.shape[1]
+    q = _c(queries, np.float32).reshape(-1, d)
+    cand = _c(candidates, NEIGHBOR).reshape(q.shape[0], -1)
+    out = np.empty((q.shape[0], k), dtype=NEIGHBOR)
+    if use_ref:
+        ref().vkref_rerank_exact(base.ctypes.data, d, q.ctypes.data, q.shape[0], cand.ctypes.data, cand.shape[1], k,
+                                 out.ctypes.data)
+    elif oracle().vko_rerank_exact(base.ctypes.data, d, q.ctypes.data, q.shape[0], cand.ctypes.data,
+                                   cand.shape[1], k, out.ctypes.data) != 0:
+        raise MemoryError("vko_rerank_exact failed")
     return out
 
 

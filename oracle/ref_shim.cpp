@@ -68,6 +68,11 @@ void vkref_exact_knn(const float* base, size_t n, const float* queries, size_t n
     veckern::exact_knn(base, n, queries, nq, d, k, out);
 }
 
+void vkref_rerank_exact(const float* base, size_t d, const float* queries, size_t nq, const Neighbor* candidates,
+                        size_t r, size_t k, Neighbor* out) {
+    veckern::rerank_exact(base, d, queries, nq, candidates, r, k, out);
+}
+
 // Returns -1.0 where the reference throws (k larger than a stride).
 double vkref_recall_at_k(const Neighbor* found, size_t found_stride, const int32_t* truth, size_t truth_stride,
                          size_t nq, size_t k) {

@@ -165,6 +165,27 @@ int vko_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* co
     return failed ? -1 : 0;
 }
 
+/* ---- cpu_ref.cpp:66-77: candidates with a negative id are skipped; the others are re-scored exactly. */
+int vko_rerank_exact(const float* base, size_t d, const float* queries, size_t nq, const vko_neighbor* candidates,
+                     size_t r, size_t k, vko_neighbor* out) {
+    int failed = 0;
+#pragma omp parallel for schedule(static)
+    for (long long q = 0; q < (long long)nq; ++q) {
+        vko_topk top;
+        if (vko_topk_init(&top, k) != 0) {
+            failed = 1;
+            continue;
+        }
+        for (size_t j = 0; j < r; ++j) {
+            const int32_t id = candidates[(size_t)q * r + j].id;
+            if (id >= 0) vko_topk_push(&top, vko_l2sq(queries + (size_t)q * d, base + (size_t)id * d, d), id);
+        }
+        vko_topk_write(&top, out + (size_t)q * k);
+        vko_topk_free(&top);
+    }
+    return failed ? -1 : 0;
+}
+
 /* ---- binary16 (IEEE 754-2008): sign bit 15, exponent bits 14-10 (bias 15), fraction bits 9-0. */
 static uint32_t f32_bits(float x) {
     uint32_t b;

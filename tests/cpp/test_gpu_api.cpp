@@ -205,3 +205,22 @@ CASE("invalid configurations are rejected") {
 }
 
 int main() { return vktest::run(); }
+
+CASE("Reranker re-scores search candidates bit for bit like the CPU rerank_exact") {
+    auto& f = fixture();
+    const std::size_t r = 100, k = 10;
+    gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
+    std::vector<Neighbor> cand(f.nq * r);
+    searcher.search(f.queries.data(), f.nq, r, ScanVariant::FusedWarp, cand.data());
+    cand[3].id = -1;  // padding is skipped
+    std::vector<vko_neighbor> expected(f.nq * k);
+    EXPECT(vko_rerank_exact(f.base.data(), f.d, f.queries.data(), f.nq,
+                            reinterpret_cast<const vko_neighbor*>(cand.data()), r, k, expected.data()) == 0);
+    gpu::Reranker reranker(f.base.data(), f.n, f.d);
+    std::vector<Neighbor> got(f.nq * k);
+    const gpu::Timings t = reranker.rerank(f.queries.data(), f.nq, cand.data(), r, k, got.data());
+    same(got, expected, "rerank");
+    EXPECT(t.scan_ms > 0);
+    cand[5].id = static_cast<int32_t>(f.n);  // out of range
+    EXPECT_THROWS(reranker.rerank(f.queries.data(), f.nq, cand.data(), r, k, got.data()));
+}

@@ -340,3 +340,60 @@ def test_planted_fp16_mistakes_fail_the_checks():
     assert np.isinf(unscaled).any()
     good = b.adc_search_f16(cent, 32, codes, queries, 10)
     assert np.isfinite(good["dist"]).all()
+
+
+# ---------------------------------------------------------------- 6. exact re-ranking (rerank_exact)
+
+def rerank_case(seed, n=3000, d=48, nq=7, r=150, family="normal"):
+    rng = np.random.default_rng(seed)
+    if family == "ties":
+        base = rng.integers(0, 3, size=(n, d)).astype(np.float32)
+        queries = rng.integers(0, 3, size=(nq, d)).astype(np.float32)
+    else:
+        base = rng.standard_normal((n, d)).astype(np.float32)
+        queries = rng.standard_normal((nq, d)).astype(np.float32)
+    cand = np.zeros((nq, r), dtype=b.NEIGHBOR)
+    cand["id"] = rng.integers(-1, n, size=(nq, r))
+    cand["dist"] = rng.standard_normal((nq, r)).astype(np.float32)  # ignored by the re-rank
+    cand["id"][:, :3] = cand["id"][:, 3:6]  # duplicated ids are pushed twice, as the reference does
+    return base, queries, cand
+
+
+@needs_ref
+@pytest.mark.parametrize("k", [1, 10, 100, 160])
+@pytest.mark.parametrize("family", ["normal", "ties"])
+def test_rerank_equals_reference_live(k, family):
+    base, queries, cand = rerank_case(41, family=family)
+    got = b.rerank_exact(base, queries, cand, k)
+    exp = b.rerank_exact(base, queries, cand, k, use_ref=True)
+    assert (got["id"] == exp["id"]).all() and (bits(got["dist"]) == bits(exp["dist"])).all()
+
+
+@pytest.mark.parametrize("k", [1, 10, 160])
+def test_rerank_equals_numpy_brute_force(k):
+    base, queries, cand = rerank_case(42)
+    got = b.rerank_exact(base, queries, cand, k)
+    for q in range(queries.shape[0]):
+        ids = cand["id"][q][cand["id"][q] >= 0]
+        # l2sq's order: float32 diff, square, add, in dimension order
+        acc = np.zeros(ids.size, dtype=np.float32)
+        for j in range(base.shape[1]):
+            diff = (queries[q, j] - base[ids, j]).astype(np.float32)
+            acc = (acc + (diff * diff).astype(np.float32)).astype(np.float32)
+        order = np.lexsort((ids, acc))[:k]
+        exp_d = np.full(k, np.inf, dtype=np.float32)
+        exp_i = np.full(k, -1, dtype=np.int32)
+        exp_d[:order.size], exp_i[:order.size] = acc[order], ids[order]
+        assert (got["id"][q] == exp_i).all() and (bits(got["dist"][q]) == bits(exp_d)).all()
+
+
+def test_rerank_of_the_exact_candidates_is_the_exact_knn():
+    # invariant: re-ranking all n ids gives the exhaustive exact k-NN (exact_knn, cpu_ref.cpp:56-64)
+    base, queries, _ = rerank_case(43, n=500)
+    allc = np.zeros((queries.shape[0], 500), dtype=b.NEIGHBOR)
+    allc["id"] = np.arange(500)
+    got = b.rerank_exact(base, queries, allc, 20)
+    d64 = ((queries.astype(np.float64)[:, None, :] - base.astype(np.float64)[None]) ** 2).sum(-1)
+    for q in range(queries.shape[0]):
+        assert set(got["id"][q]) == set(np.argsort(d64[q], kind="stable")[:20]) or \
+            np.allclose(np.sort(d64[q])[:20], got["dist"][q], rtol=1e-5)

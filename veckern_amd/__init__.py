@@ -18,7 +18,7 @@ import numpy as np
 __all__ = [
     "ScanVariant", "Tuning", "Timings", "LaunchShape", "DeviceInfo", "PQSearcher", "VkError",
     "variant_name", "is_fused", "needs_m16", "device_info", "device_count", "dispatched_k", "validate_tuning",
-    "library", "LIB_PATH", "DeviceArray",
+    "library", "LIB_PATH", "DeviceArray", "Reranker",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -110,6 +110,12 @@ _SIGNATURES = {
                                  ctypes.POINTER(_Timings)]),
     "vk_distances": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P, ctypes.POINTER(_Timings)]),
     "vk_search_device": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P,
+                                        ctypes.POINTER(_Timings)]),
+    "vk_reranker_create": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(_P)]),
+    "vk_reranker_destroy": (None, [_P]),
+    "vk_rerank": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.c_size_t, _P,
+                                 ctypes.POINTER(_Timings)]),
+    "vk_rerank_device": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.c_size_t, _P,
                                         ctypes.POINTER(_Timings)]),
 }
 
@@ -320,6 +326,58 @@ class PQSearcher:
         t = _Timings()
         _check(library().vk_search_device(self._h, ctypes.c_void_p(d_queries), nq, k, int(variant),
                                           ctypes.c_void_p(d_out), ctypes.byref(t)))
+        return _timings(t)
+
+
+class Reranker:
+    """Exact re-ranking on the GPU (the reference's CPU rerank_exact, cpu_ref.cpp:66-77): base vectors float32
+    n x d are copied to the device once; rerank() re-scores nq x r candidates (NEIGHBOR_DTYPE records, ids < 0
+    skipped) with the exact squared L2 distance and keeps the k smallest by (dist, id).
+    """
+
+    def __init__(self, base: np.ndarray):
+        lib = library()
+        b = np.ascontiguousarray(base, dtype=np.float32)
+        if b.ndim != 2:
+            raise ValueError("base must be n x d")
+        self.n, self.d = b.shape
+        self._h = ctypes.c_void_p()
+        _check(lib.vk_reranker_create(b.ctypes.data, self.n, self.d, ctypes.byref(self._h)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            library().vk_reranker_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def rerank(self, queries: np.ndarray, candidates: np.ndarray, k: int):
+        """Returns (dist [nq, k] float32, ids [nq, k] int32, Timings)."""
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.d)
+        c = np.ascontiguousarray(candidates, dtype=NEIGHBOR_DTYPE)
+        if c.ndim != 2 or c.shape[0] != q.shape[0]:
+            raise ValueError("candidates must be nq x r")
+        out = np.empty((q.shape[0], k), dtype=NEIGHBOR_DTYPE)
+        t = _Timings()
+        _check(library().vk_rerank(self._h, q.ctypes.data, q.shape[0], c.ctypes.data, c.shape[1], k,
+                                   out.ctypes.data, ctypes.byref(t)))
+        return out["dist"].copy(), out["id"].copy(), _timings(t)
+
+    def rerank_device(self, d_queries: int, nq: int, d_candidates: int, r: int, k: int, d_out: int) -> Timings:
+        """Device-resident form: queries nq x d, candidates nq x r pairs, out nq x k pairs (device addresses)."""
+        t = _Timings()
+        _check(library().vk_rerank_device(self._h, ctypes.c_void_p(d_queries), nq, ctypes.c_void_p(d_candidates),
+                                          r, k, ctypes.c_void_p(d_out), ctypes.byref(t)))
         return _timings(t)
 
 

@@ -490,6 +490,79 @@ struct vk_searcher {
 
 static_assert(sizeof(vk_neighbor) == sizeof(Pair), "vk_neighbor and the device pair must share a layout");
 
+// Exact re-ranking against base vectors held in HBM (rerank.hip). The base is copied to the device once; calls
+// stage queries and candidates in, results out (or take device pointers), on the re-ranker's own stream.
+struct vk_reranker {
+    int device = 0;
+    size_t n = 0, d = 0;
+    hipStream_t stream = nullptr;
+    DeviceBuffer<float> base, queries;
+    DeviceBuffer<Pair> candidates, out;
+    DeviceBuffer<unsigned> error;
+
+    ~vk_reranker() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    static void check(size_t r, size_t k) {
+        require(k >= 1 && k <= 128, "k must be in [1, 128]");
+        require(r >= 1, "r must be >= 1");
+    }
+
+    // d_q: nq x d, d_c: nq x r candidates, d_o: nq x k results, all on this device.
+    void run(const float* d_q, size_t nq, const Pair* d_c, size_t r, size_t k, Pair* d_o, vk_timings* t,
+             StageClock& clock) {
+        error.ensure(1);
+        VK_HIP(hipMemsetAsync(error.get(), 0, sizeof(unsigned), stream));
+        vk::RerankArgs a{};
+        a.base = base.get();
+        a.n = static_cast<int64_t>(n);
+        a.d = static_cast<int>(d);
+        a.queries = d_q;
+        a.nq = static_cast<int64_t>(nq);
+        a.candidates = d_c;
+        a.r = static_cast<int64_t>(r);
+        a.K = vk::plan::dispatched_k(k);
+        a.k = static_cast<int>(k);
+        a.out = d_o;
+        a.error = error.get();
+        clock.time(&t->scan_ms, [&] { VK_HIP(vk::launch_rerank(a, stream)); });
+    }
+
+    void finish(StageClock& clock) {
+        unsigned flag = 0;
+        VK_HIP(hipMemcpyAsync(&flag, error.get(), sizeof flag, hipMemcpyDeviceToHost, stream));
+        clock.settle();
+        if (flag) fail(VK_ERR_INVALID_ARGUMENT, "a candidate id is >= n (the number of base vectors)");
+    }
+
+    void rerank_host(const float* host_q, size_t nq, const vk_neighbor* host_c, size_t r, size_t k,
+                     vk_neighbor* host_o, vk_timings* t) {
+        VK_HIP(hipSetDevice(device));
+        StageClock clock(stream);
+        queries.ensure(nq * d);
+        candidates.ensure(nq * r);
+        out.ensure(nq * k);
+        clock.time(&t->transfer_ms, [&] {
+            VK_HIP(hipMemcpyAsync(queries.get(), host_q, nq * d * sizeof(float), hipMemcpyHostToDevice, stream));
+            VK_HIP(hipMemcpyAsync(candidates.get(), host_c, nq * r * sizeof(Pair), hipMemcpyHostToDevice, stream));
+        });
+        run(queries.get(), nq, candidates.get(), r, k, out.get(), t, clock);
+        clock.time(&t->transfer_ms, [&] {
+            VK_HIP(hipMemcpyAsync(host_o, out.get(), nq * k * sizeof(Pair), hipMemcpyDeviceToHost, stream));
+        });
+        finish(clock);
+    }
+
+    void rerank_device(const float* d_q, size_t nq, const vk_neighbor* d_c, size_t r, size_t k, vk_neighbor* d_o,
+                       vk_timings* t) {
+        VK_HIP(hipSetDevice(device));
+        StageClock clock(stream);
+        run(d_q, nq, reinterpret_cast<const Pair*>(d_c), r, k, reinterpret_cast<Pair*>(d_o), t, clock);
+        finish(clock);
+    }
+};
+
 // ------------------------------------------------------------------------------------------------ exports
 
 VK_EXPORT const char* vk_last_error(void) { return g_error.c_str(); }
@@ -611,6 +684,56 @@ VK_EXPORT int vk_search(vk_searcher* s, const float* queries, size_t nq, size_t 
             s->search_host(queries, nq, k, variant, out, &t);
         } else {
             s->check_search(k, variant);
+        }
+        if (timings) *timings = t;
+    });
+}
+
+VK_EXPORT int vk_reranker_create(const float* base, size_t n, size_t d, vk_reranker** out) {
+    return guarded([&] {
+        require(out != nullptr, "out is null");
+        *out = nullptr;
+        require(d > 0 && d <= static_cast<size_t>(std::numeric_limits<int32_t>::max()), "d must be positive");
+        require(n > 0 && n < static_cast<size_t>(std::numeric_limits<int32_t>::max()), "n must fit in int32 ids");
+        require(base != nullptr, "base must not be null");
+        auto r = std::make_unique<vk_reranker>();
+        VK_HIP(hipGetDevice(&r->device));
+        r->n = n;
+        r->d = d;
+        VK_HIP(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking));
+        r->base.ensure(n * d);
+        VK_HIP(hipMemcpy(r->base.get(), base, n * d * sizeof(float), hipMemcpyHostToDevice));
+        *out = r.release();
+    });
+}
+
+VK_EXPORT void vk_reranker_destroy(vk_reranker* r) { delete r; }
+
+VK_EXPORT int vk_rerank(vk_reranker* r, const float* queries, size_t nq, const vk_neighbor* candidates, size_t nr,
+                        size_t k, vk_neighbor* out, vk_timings* timings) {
+    return guarded([&] {
+        require(r != nullptr, "reranker is null");
+        vk_reranker::check(nr, k);
+        vk_timings t{};
+        if (nq > 0) {
+            require(queries != nullptr && candidates != nullptr && out != nullptr,
+                    "queries, candidates and out must not be null");
+            r->rerank_host(queries, nq, candidates, nr, k, out, &t);
+        }
+        if (timings) *timings = t;
+    });
+}
+
+VK_EXPORT int vk_rerank_device(vk_reranker* r, const float* d_queries, size_t nq, const vk_neighbor* d_candidates,
+                               size_t nr, size_t k, vk_neighbor* d_out, vk_timings* timings) {
+    return guarded([&] {
+        require(r != nullptr, "reranker is null");
+        vk_reranker::check(nr, k);
+        vk_timings t{};
+        if (nq > 0) {
+            require(d_queries != nullptr && d_candidates != nullptr && d_out != nullptr,
+                    "queries, candidates and out must not be null");
+            r->rerank_device(d_queries, nq, d_candidates, nr, k, d_out, &t);
         }
         if (timings) *timings = t;
     });

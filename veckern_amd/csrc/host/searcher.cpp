@@ -80,6 +80,25 @@ void PQSearcher::set_tuning(const Tuning& tuning) {
 
 const Tuning& PQSearcher::tuning() const { return impl_->tuning; }
 
+struct Reranker::Impl {
+    vk_reranker* handle = nullptr;
+    ~Impl() { vk_reranker_destroy(handle); }
+};
+
+Reranker::Reranker(const float* base, std::size_t n, std::size_t d) : impl_(std::make_unique<Impl>()) {
+    rethrow(vk_reranker_create(base, n, d, &impl_->handle));
+}
+
+Reranker::~Reranker() = default;
+
+Timings Reranker::rerank(const float* queries, std::size_t nq, const Neighbor* candidates, std::size_t r,
+                         std::size_t k, Neighbor* out) {
+    vk_timings t{};
+    rethrow(vk_rerank(impl_->handle, queries, nq, reinterpret_cast<const vk_neighbor*>(candidates), r, k,
+                      reinterpret_cast<vk_neighbor*>(out), &t));
+    return from_c(t);
+}
+
 PQSearcher::LaunchShape PQSearcher::last_launch() const {
     vk_launch_shape c{};
     rethrow(vk_searcher_last_launch(impl_->handle, &c));

@@ -102,4 +102,20 @@ struct SelectArgs {
 };
 hipError_t launch_select(const SelectArgs& a, int nq, hipStream_t stream);
 
+// ---- exact re-ranking (rerank.hip): one wave per query over its r candidates
+struct RerankArgs {
+    const float* base;        // n x d, row-major
+    int64_t n;
+    int d;
+    const float* queries;     // nq x d
+    int64_t nq;
+    const Pair* candidates;   // nq x r; ids < 0 are skipped
+    int64_t r;
+    int K;                    // list length (dispatched k)
+    int k;                    // results per query
+    Pair* out;                // nq x k; empty slots become {+inf, -1}
+    unsigned* error;          // set to non-zero when a candidate id is >= n (that candidate is not read)
+};
+hipError_t launch_rerank(const RerankArgs& a, hipStream_t stream);
+
 }  // namespace vk
