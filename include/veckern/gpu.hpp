@@ -81,6 +81,12 @@ private:
     std::unique_ptr<Impl> impl_;
 };
 
+// PQ training and encoding with the nearest-centroid searches on the GPU (not in the reference's gpu.hpp, where
+// ProductQuantizer::train / encode run on the CPU). Results are identical to pq.train(x, n, iters, seed) and
+// pq.encode(x, n, codes): the kernel keeps nearest_centroid's first-minimum rule and l2sq's arithmetic.
+void train(ProductQuantizer& pq, const float* x, std::size_t n, std::size_t iters = 20, uint64_t seed = 1);
+void encode(const ProductQuantizer& pq, const float* x, std::size_t n, uint8_t* codes);
+
 // Exact re-ranking on the GPU (not in the reference's gpu.hpp: its rerank_exact, cpu_ref.hpp:55-56, runs on the
 // CPU). The n x d base vectors are copied to the device once; rerank() takes the same arguments as rerank_exact
 // minus the base and returns bit-identical results (ids < 0 skipped; ids >= n throw std::invalid_argument).

@@ -9,6 +9,12 @@
 
 namespace veckern {
 
+// Nearest-centroid assignment of one sub-space, the inner step of train(): out[i] = index of the centroid of
+// `cent` (256 x dsub) nearest to sub-vector i of `sub` (n x dsub). gpu::train passes the GPU kernel; every
+// implementation must return the first minimum of l2sq (nearest_centroid's rule) so that training is identical.
+using AssignFn = void (*)(const float* sub, std::size_t n, const float* cent, std::size_t dsub, uint32_t* out,
+                          void* context);
+
 class ProductQuantizer {
 public:
     // Throws std::runtime_error unless d is a positive multiple of m.
@@ -18,6 +24,8 @@ public:
     // points as the initial centroids, then `iters` rounds of nearest-centroid assignment and mean update;
     // an empty cluster is re-seeded with a random training point. Deterministic for a given seed.
     void train(const float* x, std::size_t n, std::size_t iters = 20, uint64_t seed = 1);
+    // The same training with the assignment step delegated (the update, initialisation and re-seeding stay here).
+    void train(const float* x, std::size_t n, std::size_t iters, uint64_t seed, AssignFn assign, void* context);
     // codes: row-major n x m bytes, the nearest centroid of each sub-vector (lowest index on ties).
     void encode(const float* x, std::size_t n, uint8_t* codes) const;
     void decode(const uint8_t* codes, std::size_t n, float* x) const;

@@ -165,6 +165,16 @@ int vk_rerank(vk_reranker* r, const float* queries, size_t nq, const vk_neighbor
 int vk_rerank_device(vk_reranker* r, const float* d_queries, size_t nq, const vk_neighbor* d_candidates,
                      size_t r_per_query, size_t k, vk_neighbor* d_out, vk_timings* timings);
 
+/* PQ encoding on the GPU: ProductQuantizer::encode (pq.hpp:36, pq.cpp:70-75). codes[i * m + s] is the first
+ * c in 0..255 with the smallest l2sq(x_i's sub-vector s, centroids[s][c]) (nearest_centroid, pq.cpp:11-22: a
+ * running minimum from FLT_MAX, strict <, dimension order without FMA), so codes are identical to the CPU's.
+ * centroids: [m][256][d/m]; x: n x d. Host buffers (x staged in 512 MiB chunks) or device pointers. */
+int vk_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes);
+int vk_pq_encode_device(const float* d_centroids, size_t d, size_t m, const float* d_x, size_t n, uint8_t* d_codes);
+/* The assignment step of k-means training (ProductQuantizer::train, pq.cpp:52-54) for one sub-space: assign[i] =
+ * nearest of the 256 centroids (256 x dsub) to sub-vector i (sub: n x dsub). Host buffers. */
+int vk_pq_assign(const float* centroids, size_t dsub, const float* sub, size_t n, uint32_t* assign);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,7 @@ def oracle() -> ctypes.CDLL:
         lib.vko_table_shift.argtypes = [_P, _S]
         lib.vko_adc_search_f16.argtypes = [_P, _S, _S, _P, _S, _P, _S, _S, _P]
         lib.vko_rerank_exact.argtypes = [_P, _S, _P, _S, _P, _S, _S, _P]
+        lib.vko_pq_encode.argtypes = [_P, _S, _S, _P, _S, _P]
         _oracle = lib
     return _oracle
 
@@ -133,6 +134,17 @@ def adc_search_f16(centroids: np.ndarray, d: int, codes: np.ndarray, queries: np
     if rc != 0:
         raise ValueError("vko_adc_search_f16 rejected its input")
     return out
+
+
+def pq_encode(centroids: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """Nearest centroid per sub-space (the reference's ProductQuantizer::encode) of the rows of x."""
+    c = _c(centroids, np.float32)
+    m = c.shape[0]
+    x = _c(x, np.float32)
+    n, d = x.shape
+    codes = np.empty((n, m), dtype=np.uint8)
+    oracle().vko_pq_encode(c.ctypes.data, d, m, x.ctypes.data, n, codes.ctypes.data)
+    return codes
 
 
 def rerank_exact(base: np.ndarray, queries: np.ndarray, candidates: np.ndarray, k: int,
@@ -232,6 +244,15 @@ class RefPQ:
         for s in range(self.m):
             out[:, s] = self.inverse[s][codes[:, s]]
         return out
+
+    def encode(self, x: np.ndarray) -> np.ndarray:
+        """The reference's ProductQuantizer::encode, translated back to indices of the given codebook."""
+        x = _c(x, np.float32)
+        codes = np.empty((x.shape[0], self.m), dtype=np.uint8)
+        ref().vkref_pq_encode(self._h, x.ctypes.data, x.shape[0], codes.ctypes.data)
+        for s in range(self.m):
+            codes[:, s] = self.perm[s][codes[:, s]]
+        return codes
 
     def adc_search(self, codes_ref: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
         """The reference's adc_search (cpu_ref.cpp:38-54); codes must already be remapped."""

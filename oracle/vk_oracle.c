@@ -4,6 +4,7 @@
  */
 #include "vk_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -163,6 +164,27 @@ int vko_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* co
         free(lut);
     }
     return failed ? -1 : 0;
+}
+
+/* ---- pq.cpp:11-22 (nearest_centroid) and 70-75 (encode) */
+void vko_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes) {
+    const size_t dsub = d / m;
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)n; ++i)
+        for (size_t s = 0; s < m; ++s) {
+            const float* sub = x + (size_t)i * d + s * dsub;
+            const float* cent = centroids + s * VKO_KSUB * dsub;
+            size_t best = 0;
+            float best_dist = FLT_MAX;
+            for (size_t c = 0; c < VKO_KSUB; ++c) {
+                const float dist = vko_l2sq(sub, cent + c * dsub, dsub);
+                if (dist < best_dist) {
+                    best_dist = dist;
+                    best = c;
+                }
+            }
+            codes[(size_t)i * m + s] = (uint8_t)best;
+        }
 }
 
 /* ---- cpu_ref.cpp:66-77: candidates with a negative id are skipped; the others are re-scored exactly. */

@@ -16,6 +16,8 @@
  *   vko_adc_search      src/cpu/cpu_ref.cpp:38-54          LUT + scan + top-k per query, OpenMP over queries
  *   vko_recall_at_k     src/cpu/cpu_ref.cpp:79-91          mean |found[:k] ∩ set(truth[:k])| / k
  *   vko_rerank_exact    src/cpu/cpu_ref.cpp:66-77          exact l2sq of each candidate id >= 0, top-k
+ *   vko_pq_encode       src/cpu/pq.cpp:11-22, 70-75        nearest centroid per sub-space: running minimum from
+ *                                                           FLT_MAX, strict <, so the first minimum wins
  *
  * The fp16-table search (ScanVariant::FusedWarpF16, this build's own variant; the reference lists lower-precision
  * tables as a next step, README.md:219) is restated on top of the same LUT:
@@ -87,6 +89,8 @@ double vko_recall_at_k(const vko_neighbor* found, size_t found_stride, const int
 /* Pushes (dists[j], ids[j]) for j < count into a top-k of size k and writes its k results (test helper for the
  * TopK known-answer tests, cpu_ref.hpp:14-40). */
 void vko_topk_run(const float* dists, const int32_t* ids, size_t count, size_t k, vko_neighbor* out);
+/* PQ encoding: codes[i * m + s] = nearest of the 256 centroids of sub-space s (centroids [m][256][d/m]). */
+void vko_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes);
 /* Exact re-ranking: for query q, every candidates[q * r + j] with id >= 0 scored by vko_l2sq against
  * base + id * d, then the k smallest by (dist, id). out: nq x k. Returns 0, or -1 on allocation failure. */
 int vko_rerank_exact(const float* base, size_t d, const float* queries, size_t nq, const vko_neighbor* candidates,

@@ -224,3 +224,14 @@ CASE("Reranker re-scores search candidates bit for bit like the CPU rerank_exact
     cand[5].id = static_cast<int32_t>(f.n);  // out of range
     EXPECT_THROWS(reranker.rerank(f.queries.data(), f.nq, cand.data(), r, k, got.data()));
 }
+
+CASE("gpu::encode and gpu::train give the CPU encoder's codes and the CPU trainer's codebook") {
+    auto& f = fixture();
+    std::vector<uint8_t> gpu_codes(f.n * f.m);
+    gpu::encode(f.pq, f.base.data(), f.n, gpu_codes.data());
+    EXPECT(gpu_codes == f.codes);
+    ProductQuantizer cpu_pq(f.d, f.m), gpu_pq(f.d, f.m);
+    cpu_pq.train(f.base.data(), 20'000, 6, 7);
+    gpu::train(gpu_pq, f.base.data(), 20'000, 6, 7);
+    EXPECT(cpu_pq.centroids() == gpu_pq.centroids());
+}

@@ -397,3 +397,42 @@ def test_rerank_of_the_exact_candidates_is_the_exact_knn():
     for q in range(queries.shape[0]):
         assert set(got["id"][q]) == set(np.argsort(d64[q], kind="stable")[:20]) or \
             np.allclose(np.sort(d64[q])[:20], got["dist"][q], rtol=1e-5)
+
+
+# ---------------------------------------------------------------- 7. PQ encoding (nearest centroid)
+
+def numpy_encode(cent, x):
+    """float32 l2sq in dimension order for all 256 centroids, first minimum (np.argmin returns the first)."""
+    m, _, dsub = cent.shape
+    codes = np.empty((x.shape[0], m), dtype=np.uint8)
+    for s in range(m):
+        sub = x[:, s * dsub:(s + 1) * dsub]
+        acc = np.zeros((x.shape[0], 256), dtype=np.float32)
+        for j in range(dsub):
+            diff = (sub[:, j:j + 1] - cent[s][None, :, j]).astype(np.float32)
+            acc = (acc + (diff * diff).astype(np.float32)).astype(np.float32)
+        codes[:, s] = np.argmin(acc, axis=1)
+    return codes
+
+
+@pytest.mark.parametrize("family", ["normal", "ties"])
+def test_pq_encode_equals_numpy_first_minimum(family):
+    cent, _, x = random_case(51, 10, 64, 16, 3000, family)
+    if family == "ties":
+        cent[:, 17] = cent[:, 3]  # duplicated centroids: the lower index must win
+    assert (b.pq_encode(cent, x) == numpy_encode(cent, x)).all()
+
+
+@needs_ref
+def test_pq_encode_equals_reference_live():
+    # tie-free codebook, so the reference's own (permuted) centroid order cannot change the winner
+    cent, _, x = random_case(52, 10, 128, 16, 4000, "normal")
+    rpq = b.RefPQ(cent, 128)
+    assert (b.pq_encode(cent, x) == rpq.encode(x)).all()
+    rpq.close()
+
+
+def test_pq_encode_of_the_centroids_is_the_identity():
+    cent, _, _ = random_case(53, 10, 32, 8, 1, "normal")
+    x = np.ascontiguousarray(cent.transpose(1, 0, 2).reshape(256, 32))  # row c = centroid c of every sub-space
+    assert (b.pq_encode(cent, x) == np.arange(256, dtype=np.uint8)[:, None]).all()

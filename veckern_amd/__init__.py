@@ -18,7 +18,7 @@ import numpy as np
 __all__ = [
     "ScanVariant", "Tuning", "Timings", "LaunchShape", "DeviceInfo", "PQSearcher", "VkError",
     "variant_name", "is_fused", "needs_m16", "device_info", "device_count", "dispatched_k", "validate_tuning",
-    "library", "LIB_PATH", "DeviceArray", "Reranker",
+    "library", "LIB_PATH", "DeviceArray", "Reranker", "pq_encode", "pq_assign",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -111,6 +111,9 @@ _SIGNATURES = {
     "vk_distances": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P, ctypes.POINTER(_Timings)]),
     "vk_search_device": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P,
                                         ctypes.POINTER(_Timings)]),
+    "vk_pq_encode": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
+    "vk_pq_encode_device": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
+    "vk_pq_assign": (ctypes.c_int, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
     "vk_reranker_create": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(_P)]),
     "vk_reranker_destroy": (None, [_P]),
     "vk_rerank": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.c_size_t, _P,
@@ -327,6 +330,26 @@ class PQSearcher:
         _check(library().vk_search_device(self._h, ctypes.c_void_p(d_queries), nq, k, int(variant),
                                           ctypes.c_void_p(d_out), ctypes.byref(t)))
         return _timings(t)
+
+
+def pq_encode(centroids: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """GPU PQ encoding (ProductQuantizer::encode, pq.cpp:70-75): codes n x m, identical to the CPU encoder."""
+    c = np.ascontiguousarray(centroids, dtype=np.float32)
+    m = c.shape[0]
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = xs.shape
+    codes = np.empty((n, m), dtype=np.uint8)
+    _check(library().vk_pq_encode(c.ctypes.data, d, m, xs.ctypes.data, n, codes.ctypes.data))
+    return codes
+
+
+def pq_assign(centroids: np.ndarray, sub: np.ndarray) -> np.ndarray:
+    """GPU k-means assignment step for one sub-space: nearest of the 256 centroids (256 x dsub) per row of sub."""
+    c = np.ascontiguousarray(centroids, dtype=np.float32)
+    s = np.ascontiguousarray(sub, dtype=np.float32)
+    out = np.empty(s.shape[0], dtype=np.uint32)
+    _check(library().vk_pq_assign(c.ctypes.data, c.shape[-1], s.ctypes.data, s.shape[0], out.ctypes.data))
+    return out
 
 
 class Reranker:

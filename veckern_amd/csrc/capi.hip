@@ -689,6 +689,105 @@ VK_EXPORT int vk_search(vk_searcher* s, const float* queries, size_t nq, size_t 
     });
 }
 
+namespace {
+
+// Device buffers and a stream for the PQ encoder / k-means assignment entry points, one set per thread and
+// device, reused across calls (k-means calls the assignment once per iteration and sub-space).
+struct PqWorkspace {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    DeviceBuffer<float> x, centroids;
+    DeviceBuffer<uint8_t> codes;
+    DeviceBuffer<uint32_t> assign;
+    ~PqWorkspace() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+PqWorkspace& pq_workspace() {
+    thread_local PqWorkspace w;
+    int dev = 0;
+    VK_HIP(hipGetDevice(&dev));
+    if (w.device != dev) {
+        if (w.stream) (void)hipStreamDestroy(w.stream);
+        w.stream = nullptr;
+        w.x.release();
+        w.centroids.release();
+        w.codes.release();
+        w.assign.release();
+        VK_HIP(hipStreamCreateWithFlags(&w.stream, hipStreamNonBlocking));
+        w.device = dev;
+    }
+    return w;
+}
+
+// Vectors per encoding chunk: the staged floats stay under 512 MiB.
+size_t encode_chunk(size_t d) { return std::max<size_t>(1, (size_t{512} << 20) / (d * sizeof(float))); }
+
+}  // namespace
+
+VK_EXPORT int vk_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes) {
+    return guarded([&] {
+        require(m > 0 && d > 0 && d % m == 0, "d must be a positive multiple of m");
+        require(m <= 65535, "m must be <= 65535");
+        if (n == 0) return;
+        require(centroids != nullptr && x != nullptr && codes != nullptr, "centroids, x and codes must not be null");
+        PqWorkspace& w = pq_workspace();
+        const size_t dsub = d / m, chunk = std::min(n, encode_chunk(d));
+        w.centroids.ensure(m * vk::KSUB * dsub);
+        VK_HIP(hipMemcpyAsync(w.centroids.get(), centroids, m * vk::KSUB * dsub * sizeof(float),
+                              hipMemcpyHostToDevice, w.stream));
+        w.x.ensure(chunk * d);
+        w.codes.ensure(chunk * m);
+        for (size_t i0 = 0; i0 < n; i0 += chunk) {
+            const size_t b = std::min(chunk, n - i0);
+            VK_HIP(hipMemcpyAsync(w.x.get(), x + i0 * d, b * d * sizeof(float), hipMemcpyHostToDevice, w.stream));
+            vk::NearestArgs a{w.x.get(), static_cast<int64_t>(b), static_cast<int64_t>(d), static_cast<int>(m),
+                              static_cast<int>(dsub), w.centroids.get(), w.codes.get(), nullptr};
+            VK_HIP(vk::launch_nearest(a, w.stream));
+            VK_HIP(hipMemcpyAsync(codes + i0 * m, w.codes.get(), b * m, hipMemcpyDeviceToHost, w.stream));
+            VK_HIP(hipStreamSynchronize(w.stream));
+        }
+    });
+}
+
+VK_EXPORT int vk_pq_encode_device(const float* d_centroids, size_t d, size_t m, const float* d_x, size_t n,
+                                  uint8_t* d_codes) {
+    return guarded([&] {
+        require(m > 0 && d > 0 && d % m == 0, "d must be a positive multiple of m");
+        require(m <= 65535, "m must be <= 65535");
+        if (n == 0) return;
+        require(d_centroids != nullptr && d_x != nullptr && d_codes != nullptr,
+                "centroids, x and codes must not be null");
+        PqWorkspace& w = pq_workspace();
+        vk::NearestArgs a{d_x, static_cast<int64_t>(n), static_cast<int64_t>(d), static_cast<int>(m),
+                          static_cast<int>(d / m), d_centroids, d_codes, nullptr};
+        VK_HIP(vk::launch_nearest(a, w.stream));
+        VK_HIP(hipStreamSynchronize(w.stream));
+    });
+}
+
+VK_EXPORT int vk_pq_assign(const float* centroids, size_t dsub, const float* sub, size_t n, uint32_t* assign) {
+    return guarded([&] {
+        require(dsub > 0 && dsub <= static_cast<size_t>(std::numeric_limits<int32_t>::max()), "dsub must be positive");
+        if (n == 0) return;
+        require(centroids != nullptr && sub != nullptr && assign != nullptr,
+                "centroids, sub and assign must not be null");
+        PqWorkspace& w = pq_workspace();
+        w.centroids.ensure(vk::KSUB * dsub);
+        w.x.ensure(n * dsub);
+        w.assign.ensure(n);
+        VK_HIP(hipMemcpyAsync(w.centroids.get(), centroids, vk::KSUB * dsub * sizeof(float), hipMemcpyHostToDevice,
+                              w.stream));
+        VK_HIP(hipMemcpyAsync(w.x.get(), sub, n * dsub * sizeof(float), hipMemcpyHostToDevice, w.stream));
+        vk::NearestArgs a{w.x.get(), static_cast<int64_t>(n), static_cast<int64_t>(dsub), 1,
+                          static_cast<int>(dsub), w.centroids.get(), nullptr, w.assign.get()};
+        VK_HIP(vk::launch_nearest(a, w.stream));
+        VK_HIP(hipMemcpyAsync(assign, w.assign.get(), n * sizeof(uint32_t), hipMemcpyDeviceToHost, w.stream));
+        VK_HIP(hipStreamSynchronize(w.stream));
+    });
+}
+
 VK_EXPORT int vk_reranker_create(const float* base, size_t n, size_t d, vk_reranker** out) {
     return guarded([&] {
         require(out != nullptr, "out is null");

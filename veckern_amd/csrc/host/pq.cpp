@@ -16,7 +16,13 @@
 namespace veckern {
 namespace {
 
-// cent_t: [dsub][256]. Returns the index of the nearest centroid to x (first minimum).
+void transpose_sub(const float* cent, std::size_t dsub, float* cent_t) {
+    for (std::size_t c = 0; c < kSubCentroids; ++c)
+        for (std::size_t j = 0; j < dsub; ++j) cent_t[j * kSubCentroids + c] = cent[c * dsub + j];
+}
+
+// cent_t: [dsub][256]. Returns the index of the nearest centroid to x: a running minimum from FLT_MAX with a
+// strict <, so the first minimum wins (nearest_centroid, pq.cpp:11-22).
 std::size_t nearest(const float* x, const float* cent_t, std::size_t dsub, float* dist) {
     for (std::size_t c = 0; c < kSubCentroids; ++c) dist[c] = 0.f;
     for (std::size_t j = 0; j < dsub; ++j) {
@@ -28,8 +34,8 @@ std::size_t nearest(const float* x, const float* cent_t, std::size_t dsub, float
         }
     }
     std::size_t best = 0;
-    float best_dist = dist[0];
-    for (std::size_t c = 1; c < kSubCentroids; ++c)
+    float best_dist = std::numeric_limits<float>::max();
+    for (std::size_t c = 0; c < kSubCentroids; ++c)
         if (dist[c] < best_dist) {
             best_dist = dist[c];
             best = c;
@@ -37,10 +43,18 @@ std::size_t nearest(const float* x, const float* cent_t, std::size_t dsub, float
     return best;
 }
 
-void transpose_sub(const float* cent, std::size_t dsub, float* cent_t) {
-    for (std::size_t c = 0; c < kSubCentroids; ++c)
-        for (std::size_t j = 0; j < dsub; ++j) cent_t[j * kSubCentroids + c] = cent[c * dsub + j];
+void assign_on_host(const float* sub, std::size_t n, const float* cent, std::size_t dsub, uint32_t* out, void*) {
+    std::vector<float> cent_t(dsub * kSubCentroids);
+    transpose_sub(cent, dsub, cent_t.data());
+#pragma omp parallel
+    {
+        std::vector<float> dist(kSubCentroids);
+#pragma omp for schedule(static)
+        for (long long i = 0; i < static_cast<long long>(n); ++i)
+            out[i] = static_cast<uint32_t>(nearest(sub + i * dsub, cent_t.data(), dsub, dist.data()));
+    }
 }
+
 
 }  // namespace
 
@@ -55,8 +69,14 @@ void ProductQuantizer::set_centroids(const std::vector<float>& centroids) {
 }
 
 void ProductQuantizer::train(const float* x, std::size_t n, std::size_t iters, uint64_t seed) {
+    train(x, n, iters, seed, &assign_on_host, nullptr);
+}
+
+void ProductQuantizer::train(const float* x, std::size_t n, std::size_t iters, uint64_t seed, AssignFn assign_fn,
+                             void* context) {
     check(n >= kSubCentroids, "PQ training needs at least 256 vectors");
-    std::vector<float> sub(n * dsub_), cent_t(dsub_ * kSubCentroids);
+    check(assign_fn != nullptr, "assignment function is null");
+    std::vector<float> sub(n * dsub_);
     std::vector<uint32_t> assign(n);
     std::vector<std::size_t> counts(kSubCentroids), order(n);
     std::vector<double> sums(kSubCentroids * dsub_);
@@ -75,14 +95,7 @@ void ProductQuantizer::train(const float* x, std::size_t n, std::size_t iters, u
         }
 
         for (std::size_t it = 0; it < iters; ++it) {
-            transpose_sub(cent, dsub_, cent_t.data());
-#pragma omp parallel
-            {
-                std::vector<float> dist(kSubCentroids);
-#pragma omp for schedule(static)
-                for (long long i = 0; i < static_cast<long long>(n); ++i)
-                    assign[i] = static_cast<uint32_t>(nearest(sub.data() + i * dsub_, cent_t.data(), dsub_, dist.data()));
-            }
+            assign_fn(sub.data(), n, cent, dsub_, assign.data(), context);
             std::fill(sums.begin(), sums.end(), 0.0);
             std::fill(counts.begin(), counts.end(), 0);
             for (std::size_t i = 0; i < n; ++i) {

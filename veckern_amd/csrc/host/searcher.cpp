@@ -80,6 +80,20 @@ void PQSearcher::set_tuning(const Tuning& tuning) {
 
 const Tuning& PQSearcher::tuning() const { return impl_->tuning; }
 
+namespace {
+void assign_on_gpu(const float* sub, std::size_t n, const float* cent, std::size_t dsub, uint32_t* out, void*) {
+    rethrow(vk_pq_assign(cent, dsub, sub, n, out));
+}
+}  // namespace
+
+void train(ProductQuantizer& pq, const float* x, std::size_t n, std::size_t iters, uint64_t seed) {
+    pq.train(x, n, iters, seed, &assign_on_gpu, nullptr);
+}
+
+void encode(const ProductQuantizer& pq, const float* x, std::size_t n, uint8_t* codes) {
+    rethrow(vk_pq_encode(pq.centroids().data(), pq.d(), pq.m(), x, n, codes));
+}
+
 struct Reranker::Impl {
     vk_reranker* handle = nullptr;
     ~Impl() { vk_reranker_destroy(handle); }

@@ -118,4 +118,17 @@ struct RerankArgs {
 };
 hipError_t launch_rerank(const RerankArgs& a, hipStream_t stream);
 
+// ---- nearest-centroid assignment (pq_assign.hip): PQ encoding and the k-means assignment step
+struct NearestArgs {
+    const float* x;           // n vectors; sub-space s of vector i starts at x + i * x_stride + s * dsub
+    int64_t n;
+    int64_t x_stride;         // floats between consecutive vectors (d for encoding, dsub for training)
+    int m;                    // sub-spaces (grid y)
+    int dsub;
+    const float* centroids;   // [m][256][dsub]
+    uint8_t* codes;           // n x m codes, or null
+    uint32_t* assign;         // n indices (m == 1), or null
+};
+hipError_t launch_nearest(const NearestArgs& a, hipStream_t stream);
+
 }  // namespace vk
