@@ -127,6 +127,80 @@ def cpu_baseline(centroids, codes, queries, k, d, target_s=10.0):
     return rec, res
 
 
+def bench_ivf(args, centroids, codes, queries, base):
+    """IVF index on the configuration's data: coarse centroids by a few seeded Lloyd rounds (GPU assignment), then
+    timed searches (host buffers) and recall against the exhaustive PQ search and the exact ground truth."""
+    import veckern_amd as vk
+    from veckern_amd import host
+    n, d, m, nq, k, data, _, _, desc = CONFIGS[args.config]
+    if base is None:
+        raise SystemExit("--ivf-lists needs base vectors (a mixture configuration)")
+    nlist, nprobe = args.ivf_lists, args.nprobe
+    t0 = time.time()
+    rng = np.random.default_rng(1)
+    coarse = base[np.sort(rng.choice(n, size=nlist, replace=False))].copy()
+    for _ in range(2):  # Lloyd rounds: assignment on the GPU, means on the host
+        ids = vk.ivf_assign(coarse, base)
+        order = np.argsort(ids, kind="stable")
+        counts = np.bincount(ids, minlength=nlist)
+        starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+        sums = np.add.reduceat(base[order].astype(np.float64), starts[counts > 0], axis=0)
+        coarse[counts > 0] = (sums / counts[counts > 0, None]).astype(np.float32)
+    list_ids = vk.ivf_assign(coarse, base)
+    log(f"[bench] IVF: {nlist} lists built in {time.time() - t0:.1f} s; largest list {np.bincount(list_ids).max()}")
+    ix = vk.IVFIndex(coarse, centroids, codes, list_ids)
+    ix.set_tuning(vk.Tuning(queries_per_block=min(args.queries_per_block, 4)))
+    # vectors each query's probed lists hold (coarse distances as float64 on the host: only the sizes are used)
+    sizes = np.bincount(list_ids, minlength=nlist)
+    cd = ((queries.astype(np.float64)[:, None, :] - coarse.astype(np.float64)[None]) ** 2).sum(-1)
+    scanned = float(np.mean(sizes[np.argsort(cd, axis=1)[:, :nprobe]].sum(1)))
+    for _ in range(args.warmup):
+        ix.search(queries, nprobe, k)
+    totals = vk.Timings()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dist, ids_out, t = ix.search(queries, nprobe, k)
+        totals.lut_ms += t.lut_ms
+        totals.scan_ms += t.scan_ms
+        totals.select_ms += t.select_ms
+        totals.transfer_ms += t.transfer_ms
+    elapsed = time.perf_counter() - t0
+    qps = nq * args.steps / elapsed
+    shape = ix.last_launch()
+    with vk.PQSearcher(centroids, codes, d) as s:
+        s.set_tuning(vk.Tuning(queries_per_block=4))
+        _, ex_ids, _ = s.search(queries, k, vk.ScanVariant.FusedWarp)
+    overlap = float(np.mean([len(set(ids_out[q]) & set(ex_ids[q])) / k for q in range(nq)]))
+    ev = min(100, nq)
+    gt = host.exact_knn(base, queries[:ev], k)
+    out = np.empty((ev, k), dtype=vk.NEIGHBOR_DTYPE)
+    out["dist"], out["id"] = dist[:ev], ids_out[:ev]
+    rec = host.recall_at_k(out, gt["id"], k)
+    ex = np.empty((ev, k), dtype=vk.NEIGHBOR_DTYPE)
+    ex["id"] = ex_ids[:ev]
+    rec_ex = host.recall_at_k(ex, gt["id"], k)
+    step_ms = elapsed * 1e3 / args.steps
+    log(f"[bench] IVF nprobe={nprobe}: {step_ms:.3f} ms/step, {qps:,.0f} queries/s; per step probe "
+        f"{totals.lut_ms / args.steps:.3f} + scan {totals.scan_ms / args.steps:.3f} + merge "
+        f"{totals.select_ms / args.steps:.3f} + copies {totals.transfer_ms / args.steps:.3f} ms; top-{k} overlap "
+        f"with the exhaustive search {overlap:.4f}; recall@{k} {rec:.4f} (exhaustive {rec_ex:.4f}); "
+        f"{scanned:,.0f} vectors scanned per query ({scanned / n * 100:.2f} %)")
+    record = {
+        "metric": f"queries/s, IVF-PQ ({nlist} lists, nprobe {nprobe}), host buffers",
+        "value": qps, "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": step_ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic: the configuration's seeded mixture; coarse centroids from 2 Lloyd rounds",
+        "config": {"workload": desc + f", IVF {nlist} lists, nprobe {nprobe}", "n": n, "d": d, "m": m, "nq": nq,
+                   "k": k, "queries_per_block": shape.queries_per_block, "blocks": shape.blocks_x},
+        "stage_ms": {"probe": totals.lut_ms / args.steps, "scan": totals.scan_ms / args.steps,
+                     "merge": totals.select_ms / args.steps, "transfer": totals.transfer_ms / args.steps},
+        "topk_overlap_with_exhaustive": overlap, "recall_at_k": rec, "recall_at_k_exhaustive": rec_ex,
+        "vectors_scanned_per_query": scanned,
+    }
+    ix.close()
+    print(json.dumps(record), flush=True)
+
+
 def load_traffic(cfg):
     """HBM bytes per scan launch measured with rocprofv3 --pmc (profiles/traffic.json), if recorded."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -149,6 +223,9 @@ def main():
     ap.add_argument("--blocks-per-query", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and its parity check")
     ap.add_argument("--no-recall", action="store_true", help="skip the exact ground truth and recall")
+    ap.add_argument("--ivf-lists", type=int, default=0, metavar="NLIST",
+                    help="instead of the exhaustive search, time the IVF index (NLIST coarse lists) on the same data")
+    ap.add_argument("--nprobe", type=int, default=32, help="lists probed per query with --ivf-lists")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run one plain device copy of BYTES (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -173,6 +250,8 @@ def main():
     variant = next(v for v in vk.ScanVariant if vk.variant_name(v).startswith(args.variant))
     n, d, m, nq, k, data, _, _, desc = CONFIGS[args.config]
     centroids, codes, queries, base = make_workload(args.config)
+    if args.ivf_lists:
+        return bench_ivf(args, centroids, codes, queries, base)
 
     floors, hbm_gbs = microbench()
     best_qg = max(floors, key=floors.get)

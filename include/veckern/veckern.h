@@ -94,6 +94,7 @@ typedef struct vk_device_info {
 
 typedef struct vk_searcher vk_searcher;
 typedef struct vk_reranker vk_reranker;
+typedef struct vk_ivf vk_ivf;
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* vk_last_error(void);
@@ -164,6 +165,27 @@ int vk_rerank(vk_reranker* r, const float* queries, size_t nq, const vk_neighbor
 /* Device pointers on the re-ranker's device (for instance the output of vk_search_device). */
 int vk_rerank_device(vk_reranker* r, const float* d_queries, size_t nq, const vk_neighbor* d_candidates,
                      size_t r_per_query, size_t k, vk_neighbor* d_out, vk_timings* timings);
+
+/* Inverted-file (IVF) PQ search: the reference's "IVF coarse partitioning" next step (README.md:219), which it
+ * does not implement. The index holds nlist coarse centroids (nlist x d), the PQ codebook ([m][256][d/m]) and the
+ * PQ codes of the n base vectors (row-major n x m, codes of the raw vectors, not residuals) grouped by
+ * list_ids[i] (each in [0, nlist), e.g. the nearest coarse centroid). A search takes, per query, the nprobe lists
+ * whose coarse centroids are nearest (exact squared L2, ties to the lower list id) and returns the k best vectors
+ * of those lists by (ADC distance, id), padded {+inf, -1}: the exhaustive search (vk_search) restricted to the
+ * probed lists, with bit-identical distances. m % 16 == 0; nprobe in [1, min(128, nlist)]; k in [1, min(128, n)].
+ * Timings: lut_ms = coarse probe kernel, scan_ms = list scan, select_ms = merge, transfer_ms = host copies
+ * (queries, per-search list grouping built on the host, results). */
+int vk_ivf_create(const float* coarse, size_t nlist, const float* centroids, size_t d, size_t m, const uint8_t* codes,
+                  const int32_t* list_ids, size_t n, vk_ivf** out);
+void vk_ivf_destroy(vk_ivf* index);
+/* Index building helper: list_ids[i] = the coarse centroid nearest to x_i (exact squared L2, the lower index on
+ * ties; 0 if every distance is NaN). coarse: nlist x d, x: n x d host buffers. */
+int vk_ivf_assign(const float* coarse, size_t nlist, size_t d, const float* x, size_t n, int32_t* list_ids);
+/* Queries per slab (queries_per_block, capped at 4) is the tuning field that applies; default 4. */
+int vk_ivf_set_tuning(vk_ivf* index, const vk_tuning* t);
+int vk_ivf_last_launch(const vk_ivf* index, vk_launch_shape* out);
+int vk_ivf_search(vk_ivf* index, const float* queries, size_t nq, size_t nprobe, size_t k, vk_neighbor* out,
+                  vk_timings* timings);
 
 /* PQ encoding on the GPU: ProductQuantizer::encode (pq.hpp:36, pq.cpp:70-75). codes[i * m + s] is the first
  * c in 0..255 with the smallest l2sq(x_i's sub-vector s, centroids[s][c]) (nearest_centroid, pq.cpp:11-22: a

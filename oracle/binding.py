@@ -44,6 +44,7 @@ def oracle() -> ctypes.CDLL:
         lib.vko_adc_search_f16.argtypes = [_P, _S, _S, _P, _S, _P, _S, _S, _P]
         lib.vko_rerank_exact.argtypes = [_P, _S, _P, _S, _P, _S, _S, _P]
         lib.vko_pq_encode.argtypes = [_P, _S, _S, _P, _S, _P]
+        lib.vko_ivf_search.argtypes = [_P, _S, _P, _S, _S, _P, _P, _S, _P, _S, _S, _S, _P]
         _oracle = lib
     return _oracle
 
@@ -133,6 +134,22 @@ def adc_search_f16(centroids: np.ndarray, d: int, codes: np.ndarray, queries: np
                                      out.ctypes.data)
     if rc != 0:
         raise ValueError("vko_adc_search_f16 rejected its input")
+    return out
+
+
+def ivf_search(coarse: np.ndarray, centroids: np.ndarray, d: int, codes: np.ndarray, list_ids: np.ndarray,
+               queries: np.ndarray, nprobe: int, k: int) -> np.ndarray:
+    """IVF search: the exhaustive search restricted to each query's nprobe nearest lists."""
+    co = _c(coarse, np.float32).reshape(-1, d)
+    c = _c(centroids, np.float32)
+    codes = _c(codes, np.uint8)
+    n, m = codes.shape
+    li = _c(list_ids, np.int32)
+    q = _c(queries, np.float32).reshape(-1, d)
+    out = np.empty((q.shape[0], k), dtype=NEIGHBOR)
+    if oracle().vko_ivf_search(co.ctypes.data, co.shape[0], c.ctypes.data, d, m, codes.ctypes.data, li.ctypes.data,
+                               n, q.ctypes.data, q.shape[0], nprobe, k, out.ctypes.data) != 0:
+        raise ValueError("vko_ivf_search rejected its input")
     return out
 
 

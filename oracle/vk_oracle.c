@@ -166,6 +166,58 @@ int vko_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* co
     return failed ? -1 : 0;
 }
 
+/* ---- IVF: the probe is a top-nprobe over the coarse centroids by (l2sq, list id); the scan of the probed lists is
+ * cpu_ref.cpp:38-54's, in id order. */
+int vko_ivf_search(const float* coarse, size_t nlist, const float* centroids, size_t d, size_t m, const uint8_t* codes,
+                   const int32_t* list_ids, size_t n, const float* queries, size_t nq, size_t nprobe, size_t k,
+                   vko_neighbor* out) {
+    if (m == 0 || d == 0 || d % m != 0 || nprobe == 0 || nprobe > nlist) return -1;
+    int failed = 0;
+#pragma omp parallel for schedule(dynamic)
+    for (long long q = 0; q < (long long)nq; ++q) {
+        const float* x = queries + (size_t)q * d;
+        float* lut = (float*)malloc(m * VKO_KSUB * sizeof(float));
+        vko_neighbor* probes = (vko_neighbor*)malloc(nprobe * sizeof(vko_neighbor));
+        unsigned char* probed = (unsigned char*)calloc(nlist, 1);
+        vko_topk near, top;
+        int ok_near = 0, ok_top = 0;
+        if (lut && probes && probed) {
+            ok_near = vko_topk_init(&near, nprobe) == 0;
+            ok_top = ok_near && vko_topk_init(&top, k) == 0;
+        }
+        if (!ok_top) {
+            if (ok_near) vko_topk_free(&near);
+            free(lut);
+            free(probes);
+            free(probed);
+            failed = 1;
+            continue;
+        }
+        for (size_t l = 0; l < nlist; ++l) vko_topk_push(&near, vko_l2sq(x, coarse + l * d, d), (int32_t)l);
+        vko_topk_write(&near, probes);
+        for (size_t p = 0; p < nprobe; ++p)
+            if (probes[p].id >= 0) probed[probes[p].id] = 1;
+        const size_t dsub = d / m;
+        for (size_t s = 0; s < m; ++s)
+            for (size_t c = 0; c < VKO_KSUB; ++c)
+                lut[s * VKO_KSUB + c] = vko_l2sq(x + s * dsub, centroids + (s * VKO_KSUB + c) * dsub, dsub);
+        for (size_t i = 0; i < n; ++i) {
+            if (!probed[list_ids[i]]) continue;
+            const uint8_t* code = codes + i * m;
+            float acc = 0.f;
+            for (size_t s = 0; s < m; ++s) acc += lut[s * VKO_KSUB + code[s]];
+            vko_topk_push(&top, acc, (int32_t)i);
+        }
+        vko_topk_write(&top, out + (size_t)q * k);
+        vko_topk_free(&near);
+        vko_topk_free(&top);
+        free(lut);
+        free(probes);
+        free(probed);
+    }
+    return failed ? -1 : 0;
+}
+
 /* ---- pq.cpp:11-22 (nearest_centroid) and 70-75 (encode) */
 void vko_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes) {
     const size_t dsub = d / m;

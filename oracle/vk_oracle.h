@@ -16,6 +16,9 @@
  *   vko_adc_search      src/cpu/cpu_ref.cpp:38-54          LUT + scan + top-k per query, OpenMP over queries
  *   vko_recall_at_k     src/cpu/cpu_ref.cpp:79-91          mean |found[:k] ∩ set(truth[:k])| / k
  *   vko_rerank_exact    src/cpu/cpu_ref.cpp:66-77          exact l2sq of each candidate id >= 0, top-k
+ *   vko_ivf_search      (no reference code: README.md:219 lists IVF as a next step) the exhaustive search of
+ *                       cpu_ref.cpp:38-54 restricted to the nprobe lists whose coarse centroids are nearest by
+ *                       (l2sq, list id)
  *   vko_pq_encode       src/cpu/pq.cpp:11-22, 70-75        nearest centroid per sub-space: running minimum from
  *                                                           FLT_MAX, strict <, so the first minimum wins
  *
@@ -89,6 +92,11 @@ double vko_recall_at_k(const vko_neighbor* found, size_t found_stride, const int
 /* Pushes (dists[j], ids[j]) for j < count into a top-k of size k and writes its k results (test helper for the
  * TopK known-answer tests, cpu_ref.hpp:14-40). */
 void vko_topk_run(const float* dists, const int32_t* ids, size_t count, size_t k, vko_neighbor* out);
+/* IVF search: coarse nlist x d; list_ids[i] in [0, nlist) is vector i's list; out: nq x k. Returns 0, or -1 on bad
+ * input or allocation failure. */
+int vko_ivf_search(const float* coarse, size_t nlist, const float* centroids, size_t d, size_t m, const uint8_t* codes,
+                   const int32_t* list_ids, size_t n, const float* queries, size_t nq, size_t nprobe, size_t k,
+                   vko_neighbor* out);
 /* PQ encoding: codes[i * m + s] = nearest of the 256 centroids of sub-space s (centroids [m][256][d/m]). */
 void vko_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes);
 /* Exact re-ranking: for query q, every candidates[q * r + j] with id >= 0 scored by vko_l2sq against

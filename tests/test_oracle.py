@@ -436,3 +436,49 @@ def test_pq_encode_of_the_centroids_is_the_identity():
     cent, _, _ = random_case(53, 10, 32, 8, 1, "normal")
     x = np.ascontiguousarray(cent.transpose(1, 0, 2).reshape(256, 32))  # row c = centroid c of every sub-space
     assert (b.pq_encode(cent, x) == np.arange(256, dtype=np.uint8)[:, None]).all()
+
+
+# ---------------------------------------------------------------- 8. IVF search (inverted lists)
+
+def ivf_case(seed, n=4000, d=64, m=16, nq=6, nlist=40, family="normal"):
+    cent, codes, queries = random_case(seed, n, d, m, nq, family)
+    rng = np.random.default_rng(seed + 1)
+    coarse = rng.standard_normal((nlist, d)).astype(np.float32)
+    list_ids = rng.integers(0, nlist, size=n).astype(np.int32)
+    return coarse, cent, codes, list_ids, queries
+
+
+@pytest.mark.parametrize("family", ["normal", "ties"])
+def test_ivf_probing_every_list_is_the_exhaustive_search(family):
+    coarse, cent, codes, list_ids, queries = ivf_case(61, family=family)
+    got = b.ivf_search(coarse, cent, 64, codes, list_ids, queries, 40, 25)
+    exp = b.adc_search(cent, 64, codes, queries, 25)
+    assert (got["id"] == exp["id"]).all() and (bits(got["dist"]) == bits(exp["dist"])).all()
+
+
+@pytest.mark.parametrize("nprobe", [1, 3, 17])
+def test_ivf_equals_numpy_restatement(nprobe):
+    coarse, cent, codes, list_ids, queries = ivf_case(62)
+    got = b.ivf_search(coarse, cent, 64, codes, list_ids, queries, nprobe, 12)
+    lut = numpy_lut(cent, queries)
+    dists = numpy_scan(lut, codes)
+    for q in range(queries.shape[0]):
+        cd = np.zeros(coarse.shape[0], dtype=np.float32)
+        for j in range(64):  # l2sq in dimension order
+            diff = (queries[q, j] - coarse[:, j]).astype(np.float32)
+            cd = (cd + (diff * diff).astype(np.float32)).astype(np.float32)
+        probed = np.lexsort((np.arange(coarse.shape[0]), cd))[:nprobe]
+        keep = np.nonzero(np.isin(list_ids, probed))[0]
+        order = keep[np.lexsort((keep, dists[q, keep]))][:12]
+        exp_d = np.full(12, np.inf, dtype=np.float32)
+        exp_i = np.full(12, -1, dtype=np.int32)
+        exp_d[:order.size], exp_i[:order.size] = dists[q, order], order
+        assert (got["id"][q] == exp_i).all() and (bits(got["dist"][q]) == bits(exp_d)).all()
+
+
+def test_ivf_one_list_is_the_exhaustive_search():
+    coarse, cent, codes, list_ids, queries = ivf_case(63, nlist=1)
+    list_ids[:] = 0
+    got = b.ivf_search(coarse, cent, 64, codes, list_ids, queries, 1, 10)
+    exp = b.adc_search(cent, 64, codes, queries, 10)
+    assert (got["id"] == exp["id"]).all() and (bits(got["dist"]) == bits(exp["dist"])).all()

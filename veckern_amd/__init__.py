@@ -18,7 +18,7 @@ import numpy as np
 __all__ = [
     "ScanVariant", "Tuning", "Timings", "LaunchShape", "DeviceInfo", "PQSearcher", "VkError",
     "variant_name", "is_fused", "needs_m16", "device_info", "device_count", "dispatched_k", "validate_tuning",
-    "library", "LIB_PATH", "DeviceArray", "Reranker", "pq_encode", "pq_assign",
+    "library", "LIB_PATH", "DeviceArray", "Reranker", "IVFIndex", "ivf_assign", "pq_encode", "pq_assign",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -111,6 +111,14 @@ _SIGNATURES = {
     "vk_distances": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P, ctypes.POINTER(_Timings)]),
     "vk_search_device": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P,
                                         ctypes.POINTER(_Timings)]),
+    "vk_ivf_create": (ctypes.c_int, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.c_size_t, _P, _P,
+                                     ctypes.c_size_t, ctypes.POINTER(_P)]),
+    "vk_ivf_destroy": (None, [_P]),
+    "vk_ivf_assign": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
+    "vk_ivf_set_tuning": (ctypes.c_int, [_P, ctypes.POINTER(_Tuning)]),
+    "vk_ivf_last_launch": (ctypes.c_int, [_P, ctypes.POINTER(_LaunchShape)]),
+    "vk_ivf_search": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _P,
+                                     ctypes.POINTER(_Timings)]),
     "vk_pq_encode": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
     "vk_pq_encode_device": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
     "vk_pq_assign": (ctypes.c_int, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
@@ -350,6 +358,74 @@ def pq_assign(centroids: np.ndarray, sub: np.ndarray) -> np.ndarray:
     out = np.empty(s.shape[0], dtype=np.uint32)
     _check(library().vk_pq_assign(c.ctypes.data, c.shape[-1], s.ctypes.data, s.shape[0], out.ctypes.data))
     return out
+
+
+def ivf_assign(coarse: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """Nearest coarse centroid (exact, lower index on ties) of every row of x, on the GPU: int32 list ids."""
+    co = np.ascontiguousarray(coarse, dtype=np.float32)
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(xs.shape[0], dtype=np.int32)
+    _check(library().vk_ivf_assign(co.ctypes.data, co.shape[0], co.shape[1], xs.ctypes.data, xs.shape[0],
+                                   out.ctypes.data))
+    return out
+
+
+class IVFIndex:
+    """Inverted-file PQ search on the GPU (vk_ivf_*): coarse float32 nlist x d, PQ centroids [m][256][d/m],
+    codes uint8 n x m (of the raw vectors), list_ids int32 n (each in [0, nlist)). search() probes each query's
+    nprobe nearest lists and returns the k best of their vectors, bit-identical to the exhaustive search restricted
+    to those lists.
+    """
+
+    def __init__(self, coarse: np.ndarray, centroids: np.ndarray, codes: np.ndarray, list_ids: np.ndarray):
+        lib = library()
+        co = np.ascontiguousarray(coarse, dtype=np.float32)
+        cent = np.ascontiguousarray(centroids, dtype=np.float32)
+        codes = np.ascontiguousarray(codes, dtype=np.uint8)
+        li = np.ascontiguousarray(list_ids, dtype=np.int32)
+        self.n, self.m = codes.shape
+        self.nlist, self.d = co.shape
+        if li.shape != (self.n,):
+            raise ValueError("list_ids must have one entry per code row")
+        self._h = ctypes.c_void_p()
+        _check(lib.vk_ivf_create(co.ctypes.data, self.nlist, cent.ctypes.data, self.d, self.m, codes.ctypes.data,
+                                 li.ctypes.data, self.n, ctypes.byref(self._h)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            library().vk_ivf_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def set_tuning(self, t: Tuning) -> None:
+        c = t._c()
+        _check(library().vk_ivf_set_tuning(self._h, ctypes.byref(c)))
+
+    def last_launch(self) -> LaunchShape:
+        s = _LaunchShape()
+        _check(library().vk_ivf_last_launch(self._h, ctypes.byref(s)))
+        return LaunchShape(s.threads, s.blocks_x, s.grid_y, s.queries_per_block, s.vectors_per_step,
+                           s.blocks_per_sm, s.waves)
+
+    def search(self, queries: np.ndarray, nprobe: int, k: int):
+        """Returns (dist [nq, k] float32, ids [nq, k] int32, Timings)."""
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.d)
+        out = np.empty((q.shape[0], k), dtype=NEIGHBOR_DTYPE)
+        t = _Timings()
+        _check(library().vk_ivf_search(self._h, q.ctypes.data, q.shape[0], nprobe, k, out.ctypes.data,
+                                       ctypes.byref(t)))
+        return out["dist"].copy(), out["id"].copy(), _timings(t)
 
 
 class Reranker:

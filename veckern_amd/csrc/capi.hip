@@ -788,6 +788,351 @@ VK_EXPORT int vk_pq_assign(const float* centroids, size_t dsub, const float* sub
     });
 }
 
+// Inverted-file index: coarse centroids, the PQ codebook, and the codes grouped by list in the word-interleaved
+// layout, each list padded to a multiple of 256 vectors (ids -1 on padding) so that a four-tile wave step never
+// crosses into the next list.
+struct vk_ivf {
+    int device = 0;
+    size_t n = 0, d = 0, m = 0, nlist = 0;
+    vk_device_info info{};
+    vk_tuning tuning{};
+    vk_launch_shape last{};
+    hipStream_t stream = nullptr;
+    DeviceBuffer<float> coarse, centroids, queries, lut;
+    DeviceBuffer<uint4> codes_v;
+    DeviceBuffer<int32_t> ids, slab_list, slab_queries, seg_len;
+    DeviceBuffer<int64_t> list_tile, slab_gran, part_offset, seg_off;
+    DeviceBuffer<Pair> probes, part, out;
+    DeviceBuffer<unsigned> error;
+    std::vector<int64_t> list_tile_h;  // [nlist + 1]
+
+    ~vk_ivf() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    void check(size_t nprobe, size_t k) const {
+        require(k >= 1 && k <= 128 && k <= n, "k must be in [1, min(128, n)]");
+        require(nprobe >= 1 && nprobe <= 128 && nprobe <= nlist, "nprobe must be in [1, min(128, nlist)]");
+    }
+
+    // d_q: nq x d device queries; d_o: nq x k device results.
+    void search(const float* d_q, size_t nq, size_t nprobe, size_t kk, Pair* d_o, vk_timings* t,
+                StageClock& clock) {
+        // 1. the nprobe nearest lists of every query: exact distances to all coarse centroids
+        probes.ensure(nq * nprobe);
+        error.ensure(1);
+        VK_HIP(hipMemsetAsync(error.get(), 0, sizeof(unsigned), stream));
+        vk::RerankArgs pa{};
+        pa.base = coarse.get();
+        pa.n = static_cast<int64_t>(nlist);
+        pa.d = static_cast<int>(d);
+        pa.queries = d_q;
+        pa.nq = static_cast<int64_t>(nq);
+        pa.candidates = nullptr;
+        pa.r = static_cast<int64_t>(nlist);
+        pa.K = vk::plan::dispatched_k(nprobe);
+        pa.k = static_cast<int>(nprobe);
+        pa.out = probes.get();
+        pa.error = error.get();
+        lut.ensure(nq * m * vk::KSUB);
+        clock.time(&t->lut_ms, [&] {
+            VK_HIP(vk::launch_rerank(pa, stream));
+            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(nq),
+                                  1, static_cast<int>(nq), lut.get(), stream));
+        });
+        std::vector<Pair> probe_h(nq * nprobe);
+        VK_HIP(hipMemcpyAsync(probe_h.data(), probes.get(), probe_h.size() * sizeof(Pair), hipMemcpyDeviceToHost,
+                              stream));
+        clock.settle();
+
+        // 2. slabs: for each list, the queries probing it in groups of up to Q
+        const int K = vk::plan::dispatched_k(kk);
+        const int segments = K <= vk::WAVE ? 1 : 2;
+        const int q = std::min(4, vk::plan::cap_q_by_batch(
+                                      vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block,
+                                                            false, K), nq));
+        const vk::WaveScanKernel kern = vk::ivf_kernel(q, static_cast<int>(m), segments);
+        if (!kern.fn) fail(VK_ERR_LOGIC, "no IVF kernel built for this (Q, m, K)");
+        const int W = kern.threads / vk::WAVE;
+        std::vector<int64_t> per_list(nlist + 1, 0);
+        for (const Pair& p : probe_h)
+            if (p.i >= 0) ++per_list[p.i + 1];  // a query whose distances are all NaN probes nothing
+        for (size_t l = 0; l < nlist; ++l) per_list[l + 1] += per_list[l];
+        std::vector<int32_t> by_list(probe_h.size());  // (query, probe) pairs ordered by list, then query
+        {
+            std::vector<int64_t> fill(per_list.begin(), per_list.end() - 1);
+            for (size_t i = 0; i < probe_h.size(); ++i)
+                if (probe_h[i].i >= 0) by_list[fill[probe_h[i].i]++] = static_cast<int32_t>(i);
+        }
+        std::vector<int32_t> s_list, s_queries;
+        std::vector<int64_t> s_gran{0};
+        std::vector<int64_t> pair_slab(probe_h.size(), -1);  // slab and slot of every (query, probe)
+        std::vector<int32_t> pair_pos(probe_h.size(), 0);
+        for (size_t l = 0; l < nlist; ++l) {
+            const int64_t tiles = list_tile_h[l + 1] - list_tile_h[l];
+            if (tiles == 0) continue;  // an empty list contributes nothing
+            for (int64_t j = per_list[l]; j < per_list[l + 1]; j += q) {
+                const int64_t slab = static_cast<int64_t>(s_list.size());
+                s_list.push_back(static_cast<int32_t>(l));
+                for (int u = 0; u < q; ++u) {
+                    const int64_t jj = j + u;
+                    if (jj < per_list[l + 1]) {
+                        const int32_t pr = by_list[jj];
+                        s_queries.push_back(pr / static_cast<int32_t>(nprobe));
+                        pair_slab[pr] = slab;
+                        pair_pos[pr] = u;
+                    } else {
+                        s_queries.push_back(-1);
+                    }
+                }
+                s_gran.push_back(s_gran.back() + tiles / 4);
+            }
+        }
+        const int64_t n_slabs = static_cast<int64_t>(s_list.size());
+        const int64_t total = s_gran.back();
+
+        // 3. balanced partition of all granules, partial-list offsets, and each query's merge segments
+        int per_cu = 0;
+        const size_t smem = kern.dynamic_lds ? static_cast<size_t>(q) * m * vk::KSUB * sizeof(float) : 0;
+        if (kern.dynamic_lds)
+            VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+        VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
+        per_cu = std::max(per_cu, 1);
+        const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(per_cu) * info.sm_count,
+                                                                      total));
+        std::vector<int32_t> count(n_slabs);
+        int max_count = 0;
+        for (int64_t s = 0; s < n_slabs; ++s) {
+            const int64_t lo = vk::first_block_of(s_gran[s], grid, total);
+            count[s] = static_cast<int32_t>(vk::first_block_of(s_gran[s + 1] - 1, grid, total) - lo + 1);
+            max_count = std::max(max_count, count[s]);
+        }
+        const int lpb = max_count > 8 ? 1 : W;
+        std::vector<int64_t> p_off(n_slabs);
+        int64_t pairs = 0;
+        for (int64_t s = 0; s < n_slabs; ++s) {
+            p_off[s] = pairs;
+            pairs += static_cast<int64_t>(q) * count[s] * lpb * K;
+        }
+        std::vector<int64_t> g_off(probe_h.size(), 0);
+        std::vector<int32_t> g_len(probe_h.size(), 0);
+        for (size_t i = 0; i < probe_h.size(); ++i) {
+            const int64_t s = pair_slab[i];
+            if (s < 0) continue;
+            const int64_t per_query = static_cast<int64_t>(count[s]) * lpb * K;
+            g_off[i] = p_off[s] + pair_pos[i] * per_query;
+            g_len[i] = static_cast<int32_t>(per_query);
+        }
+
+        last = vk_launch_shape{};
+        last.threads = kern.threads;
+        last.blocks_x = static_cast<int>(grid);
+        last.grid_y = 1;
+        last.queries_per_block = q;
+        last.vectors_per_step = 4;
+        last.blocks_per_sm = per_cu;
+        last.waves = static_cast<double>(grid) / (static_cast<double>(per_cu) * info.sm_count);
+
+        part.ensure(static_cast<size_t>(std::max<int64_t>(pairs, 1)));
+        seg_off.ensure(g_off.size());
+        seg_len.ensure(g_len.size());
+        if (n_slabs > 0) {
+            slab_list.ensure(s_list.size());
+            slab_queries.ensure(s_queries.size());
+            slab_gran.ensure(s_gran.size());
+            part_offset.ensure(p_off.size());
+            clock.time(&t->transfer_ms, [&] {
+                VK_HIP(hipMemcpyAsync(slab_list.get(), s_list.data(), s_list.size() * sizeof(int32_t),
+                                      hipMemcpyHostToDevice, stream));
+                VK_HIP(hipMemcpyAsync(slab_queries.get(), s_queries.data(), s_queries.size() * sizeof(int32_t),
+                                      hipMemcpyHostToDevice, stream));
+                VK_HIP(hipMemcpyAsync(slab_gran.get(), s_gran.data(), s_gran.size() * sizeof(int64_t),
+                                      hipMemcpyHostToDevice, stream));
+                VK_HIP(hipMemcpyAsync(part_offset.get(), p_off.data(), p_off.size() * sizeof(int64_t),
+                                      hipMemcpyHostToDevice, stream));
+            });
+        }
+        clock.time(&t->transfer_ms, [&] {
+            VK_HIP(hipMemcpyAsync(seg_off.get(), g_off.data(), g_off.size() * sizeof(int64_t), hipMemcpyHostToDevice,
+                                  stream));
+            VK_HIP(hipMemcpyAsync(seg_len.get(), g_len.data(), g_len.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+                                  stream));
+        });
+
+        // 4. the scan over the probed lists, then the per-query merge
+        if (total > 0) {
+            vk::WaveScanArgs a{};
+            a.queries = d_q;
+            a.centroids = centroids.get();
+            a.codes = codes_v.get();
+            a.n = static_cast<int64_t>(n);
+            a.d = static_cast<int>(d);
+            a.m = static_cast<int>(m);
+            a.nq = static_cast<int>(nq);
+            a.K = K;
+            a.k = static_cast<int>(kk);
+            a.total = total;
+            a.lists_per_block = lpb;
+            a.part = part.get();
+            a.n_slabs = n_slabs;
+            a.slab_gran = slab_gran.get();
+            a.slab_list = slab_list.get();
+            a.slab_queries = slab_queries.get();
+            a.list_tile = list_tile.get();
+            a.ids = ids.get();
+            a.part_offset = part_offset.get();
+            a.lut = lut.get();
+            clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(grid), smem, stream)); });
+        }
+        vk::IvfMergeArgs ma{part.get(), seg_off.get(), seg_len.get(), static_cast<int>(nprobe),
+                            static_cast<int64_t>(nq), K, static_cast<int>(kk), d_o};
+        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_ivf_merge(ma, stream)); });
+    }
+};
+
+VK_EXPORT int vk_ivf_create(const float* coarse, size_t nlist, const float* centroids, size_t d, size_t m,
+                            const uint8_t* codes, const int32_t* list_ids, size_t n, vk_ivf** out) {
+    return guarded([&] {
+        require(out != nullptr, "out is null");
+        *out = nullptr;
+        require(m > 0 && d > 0 && d % m == 0, "d must be a positive multiple of m");
+        require(m % 16 == 0, "the IVF scan requires m % 16 == 0");
+        require(n > 0 && n < static_cast<size_t>(std::numeric_limits<int32_t>::max()), "n must fit in int32 ids");
+        require(nlist > 0 && nlist < static_cast<size_t>(std::numeric_limits<int32_t>::max()), "nlist out of range");
+        require(coarse != nullptr && centroids != nullptr && codes != nullptr && list_ids != nullptr,
+                "coarse, centroids, codes and list_ids must not be null");
+        auto v = std::make_unique<vk_ivf>();
+        VK_HIP(hipGetDevice(&v->device));
+        fill_device_info(v->device, &v->info);
+        vk_tuning_default(&v->tuning);
+        v->tuning.queries_per_block = 4;
+        v->n = n;
+        v->d = d;
+        v->m = m;
+        v->nlist = nlist;
+        require(m * vk::KSUB * sizeof(float) <= v->info.max_smem_per_block, "LUT does not fit in LDS");
+        // group the vectors by list (stable in id order), each list padded to a multiple of 256 vectors
+        std::vector<int64_t> sizes(nlist, 0);
+        for (size_t i = 0; i < n; ++i) {
+            require(list_ids[i] >= 0 && static_cast<size_t>(list_ids[i]) < nlist, "list id out of range");
+            ++sizes[list_ids[i]];
+        }
+        v->list_tile_h.assign(nlist + 1, 0);
+        for (size_t l = 0; l < nlist; ++l) v->list_tile_h[l + 1] = v->list_tile_h[l] + (sizes[l] + 255) / 256 * 4;
+        const int64_t padded = v->list_tile_h[nlist] * vk::WAVE;
+        std::vector<uint8_t> rows(static_cast<size_t>(std::max<int64_t>(padded, 1)) * m, 0);
+        std::vector<int32_t> ids(static_cast<size_t>(std::max<int64_t>(padded, 1)), -1);
+        std::vector<int64_t> fill(nlist);
+        for (size_t l = 0; l < nlist; ++l) fill[l] = v->list_tile_h[l] * vk::WAVE;
+        for (size_t i = 0; i < n; ++i) {
+            const int64_t pos = fill[list_ids[i]]++;
+            std::memcpy(rows.data() + pos * m, codes + i * m, m);
+            ids[pos] = static_cast<int32_t>(i);
+        }
+        VK_HIP(hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking));
+        v->coarse.ensure(nlist * d);
+        VK_HIP(hipMemcpy(v->coarse.get(), coarse, nlist * d * sizeof(float), hipMemcpyHostToDevice));
+        v->centroids.ensure(m * vk::KSUB * (d / m));
+        VK_HIP(hipMemcpy(v->centroids.get(), centroids, m * vk::KSUB * (d / m) * sizeof(float), hipMemcpyHostToDevice));
+        v->ids.ensure(ids.size());
+        VK_HIP(hipMemcpy(v->ids.get(), ids.data(), ids.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        v->list_tile.ensure(nlist + 1);
+        VK_HIP(hipMemcpy(v->list_tile.get(), v->list_tile_h.data(), (nlist + 1) * sizeof(int64_t),
+                         hipMemcpyHostToDevice));
+        if (padded > 0) {
+            DeviceBuffer<uint8_t> staged;
+            staged.ensure(rows.size());
+            VK_HIP(hipMemcpy(staged.get(), rows.data(), rows.size(), hipMemcpyHostToDevice));
+            v->codes_v.ensure(static_cast<size_t>(padded) * (m / 16));
+            VK_HIP(vk::launch_build_words(staged.get(), padded, static_cast<int>(m), padded, v->codes_v.get(),
+                                          v->stream));
+            VK_HIP(hipStreamSynchronize(v->stream));
+        }
+        *out = v.release();
+    });
+}
+
+VK_EXPORT void vk_ivf_destroy(vk_ivf* v) { delete v; }
+
+VK_EXPORT int vk_ivf_assign(const float* coarse, size_t nlist, size_t d, const float* x, size_t n, int32_t* list_ids) {
+    return guarded([&] {
+        require(d > 0 && d <= static_cast<size_t>(std::numeric_limits<int32_t>::max()), "d must be positive");
+        require(nlist > 0 && nlist < static_cast<size_t>(std::numeric_limits<int32_t>::max()), "nlist out of range");
+        if (n == 0) return;
+        require(coarse != nullptr && x != nullptr && list_ids != nullptr, "coarse, x and list_ids must not be null");
+        PqWorkspace& w = pq_workspace();
+        const size_t chunk = std::min(n, encode_chunk(d));
+        DeviceBuffer<unsigned> error;
+        DeviceBuffer<Pair> best;
+        error.ensure(1);
+        best.ensure(chunk);
+        w.centroids.ensure(nlist * d);
+        VK_HIP(hipMemcpyAsync(w.centroids.get(), coarse, nlist * d * sizeof(float), hipMemcpyHostToDevice, w.stream));
+        w.x.ensure(chunk * d);
+        std::vector<Pair> host(chunk);
+        for (size_t i0 = 0; i0 < n; i0 += chunk) {
+            const size_t b = std::min(chunk, n - i0);
+            VK_HIP(hipMemcpyAsync(w.x.get(), x + i0 * d, b * d * sizeof(float), hipMemcpyHostToDevice, w.stream));
+            VK_HIP(hipMemsetAsync(error.get(), 0, sizeof(unsigned), w.stream));
+            // the nearest coarse centroid of each vector: a re-rank of every centroid, k = 1
+            vk::RerankArgs a{w.centroids.get(), static_cast<int64_t>(nlist), static_cast<int>(d), w.x.get(),
+                             static_cast<int64_t>(b), nullptr, static_cast<int64_t>(nlist), vk::plan::dispatched_k(1),
+                             1, best.get(), error.get()};
+            VK_HIP(vk::launch_rerank(a, w.stream));
+            VK_HIP(hipMemcpyAsync(host.data(), best.get(), b * sizeof(Pair), hipMemcpyDeviceToHost, w.stream));
+            VK_HIP(hipStreamSynchronize(w.stream));
+            for (size_t i = 0; i < b; ++i) list_ids[i0 + i] = host[i].i < 0 ? 0 : host[i].i;
+        }
+    });
+}
+
+VK_EXPORT int vk_ivf_set_tuning(vk_ivf* v, const vk_tuning* t) {
+    return guarded([&] {
+        require(v != nullptr, "index is null");
+        const int rc = vk_tuning_validate(t);
+        if (rc != VK_OK) fail(rc, g_error);
+        v->tuning = *t;
+    });
+}
+
+VK_EXPORT int vk_ivf_last_launch(const vk_ivf* v, vk_launch_shape* out) {
+    return guarded([&] {
+        require(v != nullptr && out != nullptr, "index and out must not be null");
+        *out = v->last;
+    });
+}
+
+VK_EXPORT int vk_ivf_search(vk_ivf* v, const float* queries, size_t nq, size_t nprobe, size_t k, vk_neighbor* out,
+                            vk_timings* timings) {
+    return guarded([&] {
+        require(v != nullptr, "index is null");
+        v->check(nprobe, k);
+        vk_timings t{};
+        if (nq > 0) {
+            require(queries != nullptr && out != nullptr, "queries and out must not be null");
+            VK_HIP(hipSetDevice(v->device));
+            StageClock clock(v->stream);
+            const size_t batch = 16384;  // queries per batch: the table kernel's grid and the per-search buffers
+            for (size_t q0 = 0; q0 < nq; q0 += batch) {
+                const size_t b = std::min(batch, nq - q0);
+                v->queries.ensure(b * v->d);
+                v->out.ensure(b * k);
+                clock.time(&t.transfer_ms, [&] {
+                    VK_HIP(hipMemcpyAsync(v->queries.get(), queries + q0 * v->d, b * v->d * sizeof(float),
+                                          hipMemcpyHostToDevice, v->stream));
+                });
+                v->search(v->queries.get(), b, nprobe, k, v->out.get(), &t, clock);
+                clock.time(&t.transfer_ms, [&] {
+                    VK_HIP(hipMemcpyAsync(out + q0 * k, v->out.get(), b * k * sizeof(Pair), hipMemcpyDeviceToHost,
+                                          v->stream));
+                });
+                clock.settle();
+            }
+        }
+        if (timings) *timings = t;
+    });
+}
+
 VK_EXPORT int vk_reranker_create(const float* base, size_t n, size_t d, vk_reranker** out) {
     return guarded([&] {
         require(out != nullptr, "out is null");

@@ -136,16 +136,14 @@ __device__ __forceinline__ void load_floats(const float* p, float* out) {
 // values it reads are wave-uniform (scalar loads); lane l takes centroids l, l + 64, l + 128, l + 192. With the
 // sub-vector width DSUB known at compile time, the four centroids' loads of a sub-space are issued together, so a
 // pass costs about one memory round trip per sub-space a wave handles rather than one per element. DSUB = 0: any
-// width. Padded query slots read the last real query; their entries are never used.
+// width. qrow[q]: query q's row (padded slots repeat a real query; their entries are never used).
 template <int QS, int M, int W, int DSUB, typename Sink>
-__device__ __forceinline__ void table_entries_w(const WaveScanArgs& a, int64_t slab, int wave, int lane, Sink& sink) {
+__device__ __forceinline__ void table_entries_w(const WaveScanArgs& a, const float* const (&qrow)[QS], int wave,
+                                                int lane, Sink& sink) {
 #pragma clang fp contract(off)
     constexpr int R = KSUB / WAVE;  // centroids per lane and sub-space
     const int m = M ? M : a.m;
     const int dsub = DSUB ? DSUB : a.d / m;
-    const float* qrow[QS];
-#pragma unroll
-    for (int q = 0; q < QS; ++q) qrow[q] = a.queries + std::min<int64_t>(slab * QS + q, a.nq - 1) * a.d;
     for (int s = wave; s < m; s += W) {
         const float* cbase = a.centroids + static_cast<int64_t>(s) * KSUB * dsub;
         if constexpr (DSUB > 0) {
@@ -194,19 +192,21 @@ __device__ __forceinline__ void table_entries_w(const WaveScanArgs& a, int64_t s
 
 // Sub-vector widths of d = 128 at m = 16, 32, 64 (and 64 at m = 16) get an unrolled pass; others the generic one.
 template <int QS, int M, int W, typename Sink>
-__device__ __forceinline__ void table_entries(const WaveScanArgs& a, int64_t slab, int wave, int lane, Sink& sink) {
+__device__ __forceinline__ void table_entries(const WaveScanArgs& a, const float* const (&qrow)[QS], int wave,
+                                              int lane, Sink& sink) {
     const int dsub = a.d / (M ? M : a.m);
-    if (dsub == 8) table_entries_w<QS, M, W, 8>(a, slab, wave, lane, sink);
-    else if (dsub == 4) table_entries_w<QS, M, W, 4>(a, slab, wave, lane, sink);
-    else if (dsub == 2) table_entries_w<QS, M, W, 2>(a, slab, wave, lane, sink);
-    else table_entries_w<QS, M, W, 0>(a, slab, wave, lane, sink);
+    if (dsub == 8) table_entries_w<QS, M, W, 8>(a, qrow, wave, lane, sink);
+    else if (dsub == 4) table_entries_w<QS, M, W, 4>(a, qrow, wave, lane, sink);
+    else if (dsub == 2) table_entries_w<QS, M, W, 2>(a, qrow, wave, lane, sink);
+    else table_entries_w<QS, M, W, 0>(a, qrow, wave, lane, sink);
 }
 
 // Writes the NG query-interleaved tables of a slab into LDS (`tables`, NG tables of table_bytes each). fp16 tables
 // take each query's power-of-two shift from the per-query maxima in `qmax` (raw fp32 bits).
 template <int QG, int NG, int M, int W, bool F16>
-__device__ __forceinline__ void build_tables(const WaveScanArgs& a, int64_t slab, unsigned char* tables,
-                                             int table_bytes, const unsigned* qmax, int wave, int lane) {
+__device__ __forceinline__ void build_tables(const WaveScanArgs& a, const float* const (&qrow)[QG * NG],
+                                             unsigned char* tables, int table_bytes, const unsigned* qmax, int wave,
+                                             int lane) {
     constexpr int QS = QG * NG;
     constexpr int EB = Entries<QG, F16>::kBytes;
     if constexpr (!F16) {
@@ -220,7 +220,7 @@ __device__ __forceinline__ void build_tables(const WaveScanArgs& a, int64_t slab
                 else *reinterpret_cast<float*>(dst) = acc[t];
             }
         };
-        table_entries<QS, M, W>(a, slab, wave, lane, sink);
+        table_entries<QS, M, W>(a, qrow, wave, lane, sink);
     } else {
         int shift[QS];
 #pragma unroll
@@ -242,7 +242,25 @@ __device__ __forceinline__ void build_tables(const WaveScanArgs& a, int64_t slab
                 else *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(g[0]);
             }
         };
-        table_entries<QS, M, W>(a, slab, wave, lane, sink);
+        table_entries<QS, M, W>(a, qrow, wave, lane, sink);
+    }
+}
+
+// Inverted lists: a query's table is the same for every list it probes, so the tables are computed once per
+// search into HBM ([q][s][c], lut.hip) and each slab only gathers its queries' rows into the interleaved LDS layout
+// (coalesced reads of consecutive entries, one 16-byte LDS write per entry group).
+template <int QG, int M, int T>
+__device__ __forceinline__ void gather_tables(const WaveScanArgs& a, const float* const (&lrow)[QG],
+                                              unsigned char* tables, int tid) {
+    const int entries = (M ? M : a.m) * KSUB;
+    for (int e = tid; e < entries; e += T) {
+        float v[QG];
+#pragma unroll
+        for (int q = 0; q < QG; ++q) v[q] = lrow[q][e];
+        unsigned char* dst = tables + e * QG * 4;
+        if constexpr (QG == 4) *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        else if constexpr (QG == 2) *reinterpret_cast<float2*>(dst) = make_float2(v[0], v[1]);
+        else *reinterpret_cast<float*>(dst) = v[0];
     }
 }
 
@@ -250,7 +268,8 @@ __device__ __forceinline__ void build_tables(const WaveScanArgs& a, int64_t slab
 // float order, with NaN above +inf): lane maxima, a wave reduction, one LDS atomicMax per (wave, query). qmax must
 // be zero beforehand; the caller synchronises after.
 template <int QS, int M, int W>
-__device__ __forceinline__ void table_maxima(const WaveScanArgs& a, int64_t slab, unsigned* qmax, int wave, int lane) {
+__device__ __forceinline__ void table_maxima(const WaveScanArgs& a, const float* const (&qrow)[QS], unsigned* qmax,
+                                             int wave, int lane) {
     uint32_t mx[QS];
 #pragma unroll
     for (int q = 0; q < QS; ++q) mx[q] = 0u;
@@ -258,7 +277,7 @@ __device__ __forceinline__ void table_maxima(const WaveScanArgs& a, int64_t slab
 #pragma unroll
         for (int q = 0; q < QS; ++q) mx[q] = max(mx[q], __float_as_uint(acc[q]));
     };
-    table_entries<QS, M, W>(a, slab, wave, lane, sink);
+    table_entries<QS, M, W>(a, qrow, wave, lane, sink);
 #pragma unroll
     for (int q = 0; q < QS; ++q) {
 #pragma unroll
@@ -337,7 +356,23 @@ constexpr int wave_kernel_waves_per_simd() {
     return waves < 1 ? 1 : (waves > 4 ? 4 : waves);
 }
 
-template <int QG, int NG, int U, int M, int S, int T, bool F16>
+// First slab whose granule range [slab_gran[s], slab_gran[s + 1]) contains `item` (binary search; inverted lists).
+__device__ __forceinline__ int64_t slab_of(const int64_t* slab_gran, int64_t slabs, int64_t item) {
+    int64_t lo = 0, hi = slabs - 1;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (slab_gran[mid] <= item) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// IVF: the scan runs over inverted lists. Slab s is list a.slab_list[s] for the queries a.slab_queries[s * QS ..]
+// (-1 pads; the first is always a real query), its granules are [a.slab_gran[s], a.slab_gran[s + 1]) of the
+// balanced partition, the list's padded tiles start at a.list_tile[list] in the word-interleaved codes, and the
+// vector ids come from a.ids (-1 on padding). Each (block, slab) writes its partial lists at a.part_offset[s];
+// a separate merge kernel combines a query's partial lists over all the lists it probed.
+template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF>
 __global__ void __launch_bounds__(T)
     __attribute__((amdgpu_waves_per_eu(wave_kernel_waves_per_simd<QG, NG, M, T, F16>())))
     fused_wave_kernel_t(WaveScanArgs a) {
@@ -373,18 +408,51 @@ __global__ void __launch_bounds__(T)
     const _Float16 one = opaque_half_one();
 
     for (int64_t item = start; item < end;) {
-        const int64_t slab = item / a.n_gran;
-        const int64_t g_lo = item - slab * a.n_gran;
-        const int64_t g_hi = min(end - slab * a.n_gran, a.n_gran);
+        // The slab holding `item` and its granules [slab_first, slab_next) in the balanced partition.
+        int64_t slab, slab_first, slab_next;
+        if constexpr (IVF) {
+            slab = slab_of(a.slab_gran, a.n_slabs, item);
+            slab_first = a.slab_gran[slab];
+            slab_next = a.slab_gran[slab + 1];
+        } else {
+            slab = item / a.n_gran;
+            slab_first = slab * a.n_gran;
+            slab_next = slab_first + a.n_gran;
+        }
+        const int64_t g_lo = item - slab_first;
+        const int64_t g_hi = min(end, slab_next) - slab_first;
+        // Query rows of the slab; live[q] is false for padded slots (which repeat a real query's row). lrow: the
+        // rows of the per-search tables (inverted lists).
+        const float* qrow[QS];
+        const float* lrow[QS];
+        bool live[QS];
+#pragma unroll
+        for (int q = 0; q < QS; ++q) {
+            int64_t qi;
+            if constexpr (IVF) {
+                qi = a.slab_queries[slab * QS + q];
+                live[q] = qi >= 0;
+                if (!live[q]) qi = a.slab_queries[slab * QS];
+            } else {
+                qi = slab * QS + q;
+                live[q] = qi < a.nq;
+                if (!live[q]) qi = a.nq - 1;
+            }
+            qrow[q] = a.queries + qi * a.d;
+            lrow[q] = IVF ? a.lut + qi * (M ? M : a.m) * KSUB : nullptr;
+        }
+        int64_t list_tile0 = 0;  // IVF: first tile of the slab's list
+        if constexpr (IVF) list_tile0 = a.list_tile[a.slab_list[slab]];
 
         __syncthreads();  // the previous slab's merge has finished with LDS
         if constexpr (F16) {
             if (tid < QS) qmax[tid] = 0u;
             __syncthreads();
-            table_maxima<QS, M, W>(a, slab, qmax, wave, lane);
+            table_maxima<QS, M, W>(a, qrow, qmax, wave, lane);
             __syncthreads();
         }
-        build_tables<QG, NG, M, W, F16>(a, slab, tables, table_bytes, qmax, wave, lane);
+        if constexpr (IVF && !F16 && NG == 1) gather_tables<QG, M, T>(a, lrow, tables, tid);
+        else build_tables<QG, NG, M, W, F16>(a, qrow, tables, table_bytes, qmax, wave, lane);
         if constexpr (kShareBound)
             for (int t = tid; t < QS * W; t += T) (&rank_bound[0][0])[t] = 0x7f800000u;  // +inf
         __syncthreads();
@@ -392,11 +460,10 @@ __global__ void __launch_bounds__(T)
         // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so the
         // scan loop offers every slot without a per-query test.
         WaveList<S> lists[QS];
-        const int64_t live = a.nq - slab * QS;
 #pragma unroll
         for (int q = 0; q < QS; ++q) {
             lists[q].init();
-            if (q >= live) lists[q].disable();
+            if (!live[q]) lists[q].disable();
         }
         const uint32_t n32 = static_cast<uint32_t>(a.n);  // n < 2^31: ids and tile bounds fit in 32 bits
         const int bound_rank = (a.K + W - 1) / W - 1;      // < 64: the entry lives in the lists' first register
@@ -416,7 +483,7 @@ __global__ void __launch_bounds__(T)
                 }
             }
             const int64_t tile0 = g * U;
-            const uint4* tile_codes = a.codes + tile0 * words * WAVE + lane;  // wave-uniform base + lane
+            const uint4* tile_codes = a.codes + (list_tile0 + tile0) * words * WAVE + lane;  // uniform base + lane
             // All code words of the U tiles are loaded first (the global-load ILP). The lookups then run one
             // tile at a time behind a scheduling fence, and each tile's candidates are offered before the next
             // tile starts: only one tile's LDS results and accumulators are live, which keeps the register
@@ -456,10 +523,19 @@ __global__ void __launch_bounds__(T)
                     for (int w = 0; w < words; ++w) lookup_word(tile_codes[(u * words + w) * WAVE], w);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                // Lanes holding a real vector: all of them except in the database's last tile.
-                const uint32_t first = static_cast<uint32_t>((tile0 + u) * WAVE);
-                const uint32_t id = first + static_cast<uint32_t>(lane);
-                const uint64_t valid = first + WAVE <= n32 ? ~uint64_t{0} : __builtin_amdgcn_ballot_w64(id < n32);
+                // Lanes holding a real vector: all of them except in the database's last tile (or, for inverted
+                // lists, the padding at the end of each list).
+                uint32_t id;
+                uint64_t valid;
+                if constexpr (IVF) {
+                    const int32_t vid = a.ids[(list_tile0 + tile0 + u) * WAVE + lane];
+                    id = static_cast<uint32_t>(vid);
+                    valid = __builtin_amdgcn_ballot_w64(vid >= 0);
+                } else {
+                    const uint32_t first = static_cast<uint32_t>((tile0 + u) * WAVE);
+                    id = first + static_cast<uint32_t>(lane);
+                    valid = first + WAVE <= n32 ? ~uint64_t{0} : __builtin_amdgcn_ballot_w64(id < n32);
+                }
 #pragma unroll
                 for (int q = 0; q < QS; ++q) lists[q].offer_masked(acc[q], static_cast<int32_t>(id), valid, a.K);
             }
@@ -479,9 +555,14 @@ __global__ void __launch_bounds__(T)
         // Partial lists of this (block, slab): part[slab][q][slot][list][K], the lists of one query contiguous.
         // With few blocks per slab every wave writes its own lists; with many, the block first merges its W lists
         // per query in LDS (the tables are dead by then), so the final merge reads W times fewer pairs.
-        const int slot = static_cast<int>(b - first_block_of(slab * a.n_gran, grid, a.total));
+        const int64_t lo = first_block_of(slab_first, grid, a.total);
+        const int count = static_cast<int>(first_block_of(slab_next - 1, grid, a.total) - lo + 1);
+        const int slot = static_cast<int>(b - lo);
         const int lpb = a.lists_per_block;
-        Pair* const slab_part = a.part + slab * QS * a.max_slots * lpb * static_cast<int64_t>(a.K);
+        // Uniform slabs reserve max_slots blocks each; inverted-list slabs have their own offsets and counts.
+        const int slots = IVF ? count : a.max_slots;
+        Pair* const slab_part = IVF ? a.part + a.part_offset[slab]
+                                    : a.part + slab * QS * a.max_slots * lpb * static_cast<int64_t>(a.K);
         Pair* const buf = reinterpret_cast<Pair*>(tables);  // QS * W * K pairs fit in the tables' space
         if (lpb == 1) {
             __syncthreads();  // every wave has finished reading the tables
@@ -490,19 +571,21 @@ __global__ void __launch_bounds__(T)
             __syncthreads();
 #pragma unroll
             for (int q = 0; q < QS; ++q)
-                merge_lists(buf + q * W * a.K, W, a.K, slab_part + (q * a.max_slots + slot) * a.K, tid, T);
+                merge_lists(buf + q * W * a.K, W, a.K, slab_part + (q * slots + slot) * a.K, tid, T);
         } else {
 #pragma unroll
             for (int q = 0; q < QS; ++q)
-                lists[q].store(slab_part + ((q * a.max_slots + slot) * W + wave) * a.K, a.K);
+                lists[q].store(slab_part + ((q * slots + slot) * W + wave) * a.K, a.K);
         }
 
         // The last of the slab's blocks to get here merges all its partial lists into the final results. The
         // counter is incremented with wrap-around at count - 1, so it is back at zero for the next search. The
         // agent-scope release fence after the barrier publishes the whole block's partial lists before the
         // increment; the last block's acquire fence makes every other block's lists visible to it.
-        const int64_t lo = first_block_of(slab * a.n_gran, grid, a.total);
-        const int count = static_cast<int>(first_block_of((slab + 1) * a.n_gran - 1, grid, a.total) - lo + 1);
+        if constexpr (IVF) {  // the merge kernel finishes inverted-list searches
+            item = slab_next;
+            continue;
+        }
         __syncthreads();
         if (tid == 0) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -522,25 +605,45 @@ __global__ void __launch_bounds__(T)
                                       wave, lane);
             }
         }
-        item = (slab + 1) * a.n_gran;
+        item = slab_next;
     }
 }
 
-template <int QG, int NG, int U, int M, int S, int T, bool F16>
+template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF>
 hipError_t launch_fused_wave_t(const WaveScanArgs& a, int grid, size_t smem, hipStream_t stream) {
-    hipLaunchKernelGGL((fused_wave_kernel_t<QG, NG, U, M, S, T, F16>), dim3(grid), dim3(T), smem, stream, a);
+    hipLaunchKernelGGL((fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF>), dim3(grid), dim3(T), smem, stream, a);
     return hipGetLastError();
 }
 
-template <int QG, int NG, int U, int M, int S, bool F16>
+template <int QG, int NG, int U, int M, int S, bool F16, bool IVF = false>
 WaveScanKernel make_wave_kernel() {
     constexpr int T = 512;
     WaveScanKernel k;
-    k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T, F16>);
+    k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF>);
     k.threads = T;
     k.dynamic_lds = M == 0;
-    k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T, F16>;
+    k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T, F16, IVF>;
     return k;
+}
+
+// Inverted-list instances for one M: fp32 tables, QG 1, 2, 4 in one group, four tiles per wave step (each list
+// is padded to a multiple of 256 vectors).
+template <int M>
+WaveScanKernel select_ivf_kernel(int qg, int segments) {
+    constexpr int kLds = 160 * 1024;
+#define VK_IVF_CASE(QG_)                                                                            \
+    if (qg == QG_) {                                                                                \
+        if constexpr (M == 0 || M * KSUB * Entries<QG_, false>::kBytes <= kLds) {                   \
+            if (segments == 1) return make_wave_kernel<QG_, 1, 4, M, 1, false, true>();             \
+            if (segments == 2) return make_wave_kernel<QG_, 1, 4, M, 2, false, true>();             \
+        }                                                                                           \
+        return WaveScanKernel{};                                                                    \
+    }
+    VK_IVF_CASE(1)
+    VK_IVF_CASE(2)
+    VK_IVF_CASE(4)
+#undef VK_IVF_CASE
+    return WaveScanKernel{};
 }
 
 // Instances for one M and entry type: every (QG, NG) whose tables fit in 160 KB of LDS when M is known. fp32

@@ -40,6 +40,15 @@ struct WaveScanArgs {
     Pair* part;              // [slabs][qg * ng][max_slots][lists_per_block][K]
     unsigned* counters;      // [slabs], zero between searches: blocks of a slab that have finished
     Pair* out;               // [nq][k]; empty slots become {+inf, -1}
+    // Inverted lists (IVF instances only); `n_gran` and `max_slots` are then unused.
+    int64_t n_slabs;
+    const int64_t* slab_gran;      // [n_slabs + 1] granule prefix of the slabs
+    const int32_t* slab_list;      // [n_slabs] list scanned by each slab
+    const int32_t* slab_queries;   // [n_slabs][qg] query of each slot, -1 for padding (slot 0 is always real)
+    const int64_t* list_tile;      // [lists + 1] first tile of each list in `codes` / `ids`
+    const int32_t* ids;            // [tiles * 64] vector id of each padded position, -1 for padding
+    const int64_t* part_offset;    // [n_slabs] first pair of each slab's partial lists in `part`
+    const float* lut;              // [nq][m][256] tables computed once per search (a query meets many lists)
 };
 
 struct WaveScanKernel {
@@ -51,6 +60,22 @@ struct WaveScanKernel {
 
 // Returns a kernel with fn == nullptr when the combination is not built. f16: binary16 tables (v9).
 WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16);
+// The inverted-list scan (ivf_m*.hip): fp32 tables, QG queries per slab, four tiles per wave step.
+WaveScanKernel ivf_kernel(int qg, int m, int segments);
+
+// ---- IVF final merge (ivf.hip): query q's partial lists are the segments seg_off[q * probes + p] .. + seg_len
+// (pairs) for p < probes; its k results go to out[q * k].
+struct IvfMergeArgs {
+    const Pair* part;
+    const int64_t* seg_off;
+    const int32_t* seg_len;
+    int probes;
+    int64_t nq;
+    int K;
+    int k;
+    Pair* out;
+};
+hipError_t launch_ivf_merge(const IvfMergeArgs& a, hipStream_t stream);
 
 // Blocks covering slab `slab` in the balanced partition of `total` work items over `grid` blocks
 // (block b owns items [b*total/grid, (b+1)*total/grid)).
@@ -109,7 +134,7 @@ struct RerankArgs {
     int d;
     const float* queries;     // nq x d
     int64_t nq;
-    const Pair* candidates;   // nq x r; ids < 0 are skipped
+    const Pair* candidates;   // nq x r; ids < 0 are skipped. Null: candidate j of every query is base row j
     int64_t r;
     int K;                    // list length (dispatched k)
     int k;                    // results per query

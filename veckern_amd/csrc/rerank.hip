@@ -49,13 +49,13 @@ __global__ void __launch_bounds__(kRerankThreads) rerank_kernel(RerankArgs a) {
     const int64_t q = static_cast<int64_t>(blockIdx.x) * (kRerankThreads / WAVE) + wave;
     if (q >= a.nq) return;  // wave-uniform
     const float* x = a.queries + q * a.d;
-    const Pair* cand = a.candidates + q * a.r;
+    const Pair* cand = a.candidates ? a.candidates + q * a.r : nullptr;
     WaveList<S> list;
     list.init();
     bool bad = false;
     for (int64_t base = 0; base < a.r; base += WAVE) {
         const int64_t j = base + lane;
-        const int32_t id = j < a.r ? cand[j].i : -1;
+        const int32_t id = j < a.r ? (cand ? cand[j].i : static_cast<int32_t>(j)) : -1;
         bad |= id >= a.n;  // an id past the base: reported, never read
         const bool use = id >= 0 && id < a.n;
         const float dist = use ? l2sq_row<VEC4>(x, a.base + static_cast<int64_t>(id) * a.d, a.d) : INFINITY;
