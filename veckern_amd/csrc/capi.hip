@@ -235,7 +235,9 @@ struct vk_searcher {
     // v8 / v9 (f16 tables): the wave-list scan over the balanced partition with its final merge, one launch.
     // d_q: device queries of this batch; writes b x kk results to d_out.
     void run_wave(const float* d_q, size_t b, size_t kk, bool f16, Pair* d_out, vk_timings* t, StageClock& clock) {
-        const int K = vk::plan::dispatched_k(kk);
+        // The wave lists take any length up to 128, so they hold exactly k entries: every one of k..K-1 that a
+        // rounded-up K would keep costs inserts (about K * ln(n / K) per list) and buys nothing.
+        const int K = static_cast<int>(kk);
         const int segments = K <= vk::WAVE ? 1 : 2;
         const size_t entry_bytes = f16 ? 2 : sizeof(float);
         const int q = vk::plan::cap_q_by_batch(
@@ -845,8 +847,8 @@ struct vk_ivf {
                               stream));
         clock.settle();
 
-        // 2. slabs: for each list, the queries probing it in groups of up to Q
-        const int K = vk::plan::dispatched_k(kk);
+        // 2. slabs: for each list, the queries probing it in groups of up to Q (lists of exactly k entries)
+        const int K = static_cast<int>(kk);
         const int segments = K <= vk::WAVE ? 1 : 2;
         const int q = std::min(4, vk::plan::cap_q_by_batch(
                                       vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block,
