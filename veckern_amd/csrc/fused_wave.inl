@@ -407,11 +407,15 @@ __global__ void __launch_bounds__(T)
     const int64_t start = b * a.total / grid, end = (b + 1) * a.total / grid;
     const _Float16 one = opaque_half_one();
 
+    // Inverted lists: the first slab of the block's range by binary search; every later one is the next slab
+    // (slabs are non-empty and contiguous in item order), so the search costs one chain of dependent loads per
+    // block, not one per slab.
+    int64_t next_slab = IVF && start < end ? slab_of(a.slab_gran, a.n_slabs, start) : 0;
     for (int64_t item = start; item < end;) {
         // The slab holding `item` and its granules [slab_first, slab_next) in the balanced partition.
         int64_t slab, slab_first, slab_next;
         if constexpr (IVF) {
-            slab = slab_of(a.slab_gran, a.n_slabs, item);
+            slab = next_slab++;
             slab_first = a.slab_gran[slab];
             slab_next = a.slab_gran[slab + 1];
         } else {
