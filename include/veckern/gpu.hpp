@@ -87,6 +87,31 @@ private:
 void train(ProductQuantizer& pq, const float* x, std::size_t n, std::size_t iters = 20, uint64_t seed = 1);
 void encode(const ProductQuantizer& pq, const float* x, std::size_t n, uint8_t* codes);
 
+// Inverted-file PQ search on the GPU (not in the reference, whose README lists IVF as a next step). coarse: nlist
+// x d centroids; codes: n x m PQ codes of the raw vectors (pq's codebook); list_ids[i] in [0, nlist): vector i's
+// list (for instance from assign_lists). search() probes each query's nprobe nearest lists (exact distances, lower
+// list id on ties) and returns the k best of their vectors by (ADC distance, id), padded {+inf, -1}. Requires
+// m % 16 == 0; nprobe in [1, min(128, nlist)]; k in [1, min(128, n)].
+class IVFSearcher {
+public:
+    IVFSearcher(const ProductQuantizer& pq, const float* coarse, std::size_t nlist, const uint8_t* codes,
+                const int32_t* list_ids, std::size_t n);
+    ~IVFSearcher();
+    IVFSearcher(const IVFSearcher&) = delete;
+    IVFSearcher& operator=(const IVFSearcher&) = delete;
+
+    Timings search(const float* queries, std::size_t nq, std::size_t nprobe, std::size_t k, Neighbor* out);
+    void set_tuning(const Tuning& tuning);  // queries_per_block (1, 2 or 4) is the field that applies
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+// The nearest of nlist coarse centroids (exact, lower index on ties) for each of the n vectors x (n x d).
+void assign_lists(const float* coarse, std::size_t nlist, std::size_t d, const float* x, std::size_t n,
+                  int32_t* list_ids);
+
 // Exact re-ranking on the GPU (not in the reference's gpu.hpp: its rerank_exact, cpu_ref.hpp:55-56, runs on the
 // CPU). The n x d base vectors are copied to the device once; rerank() takes the same arguments as rerank_exact
 // minus the base and returns bit-identical results (ids < 0 skipped; ids >= n throw std::invalid_argument).

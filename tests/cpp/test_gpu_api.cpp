@@ -235,3 +235,21 @@ CASE("gpu::encode and gpu::train give the CPU encoder's codes and the CPU traine
     gpu::train(gpu_pq, f.base.data(), 20'000, 6, 7);
     EXPECT(cpu_pq.centroids() == gpu_pq.centroids());
 }
+
+CASE("IVFSearcher probing every list equals the exhaustive search; fewer lists match the oracle") {
+    auto& f = fixture();
+    const std::size_t nlist = 32, k = 10;
+    std::vector<float> coarse(f.base.begin(), f.base.begin() + nlist * f.d);  // the first vectors as centroids
+    std::vector<int32_t> lists(f.n);
+    gpu::assign_lists(coarse.data(), nlist, f.d, f.base.data(), f.n, lists.data());
+    gpu::IVFSearcher ivf(f.pq, coarse.data(), nlist, f.codes.data(), lists.data(), f.n);
+    std::vector<Neighbor> got(f.nq * k);
+    ivf.search(f.queries.data(), f.nq, nlist, k, got.data());
+    same(got, oracle_search(f.pq, f.codes, f.n, f.queries.data(), f.nq, k), "ivf all lists");
+    std::vector<vko_neighbor> expected(f.nq * k);
+    EXPECT(vko_ivf_search(coarse.data(), nlist, f.pq.centroids().data(), f.d, f.m, f.codes.data(), lists.data(), f.n,
+                          f.queries.data(), f.nq, 5, k, expected.data()) == 0);
+    ivf.search(f.queries.data(), f.nq, 5, k, got.data());
+    same(got, expected, "ivf nprobe 5");
+    EXPECT_THROWS(ivf.search(f.queries.data(), f.nq, nlist + 1, k, got.data()));
+}

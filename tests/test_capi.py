@@ -48,7 +48,9 @@ def test_cpp_api_library_exports_the_searcher():
     for sym in ("veckern::gpu::PQSearcher::PQSearcher", "veckern::gpu::PQSearcher::search",
                 "veckern::gpu::PQSearcher::distances", "veckern::gpu::PQSearcher::set_tuning",
                 "veckern::gpu::PQSearcher::last_launch", "veckern::gpu::device_info", "veckern::gpu::variant_name",
-                "veckern::gpu::is_fused", "veckern::gpu::Reranker::Reranker", "veckern::gpu::Reranker::rerank"):
+                "veckern::gpu::is_fused", "veckern::gpu::Reranker::Reranker", "veckern::gpu::Reranker::rerank",
+                "veckern::gpu::IVFSearcher::IVFSearcher", "veckern::gpu::IVFSearcher::search",
+                "veckern::gpu::assign_lists", "veckern::gpu::encode", "veckern::gpu::train"):
         assert sym in out, sym
 
 

@@ -94,6 +94,35 @@ void encode(const ProductQuantizer& pq, const float* x, std::size_t n, uint8_t* 
     rethrow(vk_pq_encode(pq.centroids().data(), pq.d(), pq.m(), x, n, codes));
 }
 
+struct IVFSearcher::Impl {
+    vk_ivf* handle = nullptr;
+    ~Impl() { vk_ivf_destroy(handle); }
+};
+
+IVFSearcher::IVFSearcher(const ProductQuantizer& pq, const float* coarse, std::size_t nlist, const uint8_t* codes,
+                         const int32_t* list_ids, std::size_t n)
+    : impl_(std::make_unique<Impl>()) {
+    rethrow(vk_ivf_create(coarse, nlist, pq.centroids().data(), pq.d(), pq.m(), codes, list_ids, n, &impl_->handle));
+}
+
+IVFSearcher::~IVFSearcher() = default;
+
+Timings IVFSearcher::search(const float* queries, std::size_t nq, std::size_t nprobe, std::size_t k, Neighbor* out) {
+    vk_timings t{};
+    rethrow(vk_ivf_search(impl_->handle, queries, nq, nprobe, k, reinterpret_cast<vk_neighbor*>(out), &t));
+    return from_c(t);
+}
+
+void IVFSearcher::set_tuning(const Tuning& tuning) {
+    const vk_tuning c = to_c(tuning);
+    rethrow(vk_ivf_set_tuning(impl_->handle, &c));
+}
+
+void assign_lists(const float* coarse, std::size_t nlist, std::size_t d, const float* x, std::size_t n,
+                  int32_t* list_ids) {
+    rethrow(vk_ivf_assign(coarse, nlist, d, x, n, list_ids));
+}
+
 struct Reranker::Impl {
     vk_reranker* handle = nullptr;
     ~Impl() { vk_reranker_destroy(handle); }
