@@ -153,3 +153,15 @@ def test_invalid_k_is_rejected(searcher, fixture):
     for k in (0, 129):
         with pytest.raises(vk.VkError):
             searcher.search(queries[:1], k, vk.ScanVariant.FusedWarp)
+
+
+def test_batches_beyond_one_launch():
+    # more queries than one launch takes (65,535): two batches through the same searcher, per-slab counters and
+    # partial-list buffers reused; every result must still be exact
+    n, d, m, nq = 1_201, 32, 16, 65_535 + 4_000
+    centroids, codes, queries = datagen.random_fixture(n, d, m, nq, seed=31)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        s.set_tuning(vk.Tuning(queries_per_block=4))
+        got_d, got_i, _ = s.search(queries, 10, vk.ScanVariant.FusedWarp)
+    exp = orc.adc_search(centroids, d, codes, queries, 10)
+    assert_same(got_d, got_i, exp, "two batches")

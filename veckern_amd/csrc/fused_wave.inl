@@ -76,19 +76,27 @@ struct Entries {
                 acc[0] = add_half_lo(acc[0], v, one);
                 acc[1] = add_half_hi(acc[1], v, one);
             } else if constexpr (QG == 4) {
-                acc[0] = add_half_lo(acc[0], v.x, one);
-                acc[1] = add_half_hi(acc[1], v.x, one);
-                acc[2] = add_half_lo(acc[2], v.y, one);
-                acc[3] = add_half_hi(acc[3], v.y, one);
+                // One statement per read: the scheduler places a read's accumulations (independent, one per
+                // query) together, so no two dependent v_fma_mix_f32 sit back to back needing a wait state.
+                // Operands as in add_half_lo/hi: src0 the binary16 half selected by op_sel, src1 fp32 1.0.
+                asm("v_fma_mix_f32 %0, %4, 1.0, %0 op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %1, %4, 1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %2, %5, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %3, %5, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                    : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+                    : "v"(v.x), "v"(v.y));
             } else {
-                acc[0] = add_half_lo(acc[0], v.x, one);
-                acc[1] = add_half_hi(acc[1], v.x, one);
-                acc[2] = add_half_lo(acc[2], v.y, one);
-                acc[3] = add_half_hi(acc[3], v.y, one);
-                acc[4] = add_half_lo(acc[4], v.z, one);
-                acc[5] = add_half_hi(acc[5], v.z, one);
-                acc[6] = add_half_lo(acc[6], v.w, one);
-                acc[7] = add_half_hi(acc[7], v.w, one);
+                asm("v_fma_mix_f32 %0, %8, 1.0, %0 op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %1, %8, 1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %2, %9, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %3, %9, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %4, %10, 1.0, %4 op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %5, %10, 1.0, %5 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %6, %11, 1.0, %6 op_sel_hi:[1,0,0]\n\t"
+                    "v_fma_mix_f32 %7, %11, 1.0, %7 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                    : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]),
+                      "+v"(acc[6]), "+v"(acc[7])
+                    : "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
             }
         }
     }
@@ -508,6 +516,27 @@ __global__ void __launch_bounds__(T)
                 // 16 lookups of one code word, sub-spaces 16w .. 16w+15 in order.
                 auto lookup_word = [&](const uint4 word, const int w) {
                     const uint32_t part[4] = {word.x, word.y, word.z, word.w};
+                    if constexpr (F16 && QG >= 4) {
+                        // The word's reads are all issued before its accumulations: the one-statement-per-read
+                        // accumulations would otherwise be scheduled right behind their own read, one read in
+                        // flight at a time.
+                        V v[16 * NG];
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) {
+                            const uint32_t c = (part[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                            const int s = w * 16 + j;
+#pragma unroll
+                            for (int t = 0; t < NG; ++t)
+                                v[j * NG + t] = *reinterpret_cast<const V*>(
+                                    tables + t * table_bytes + (s * KSUB + static_cast<int>(c)) * E::kBytes);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int j = 0; j < 16; ++j)
+#pragma unroll
+                            for (int t = 0; t < NG; ++t) E::add(&acc[t * QG], v[j * NG + t], one);
+                        return;
+                    }
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
                         const uint32_t c = (part[j >> 2] >> (8 * (j & 3))) & 0xffu;
