@@ -98,3 +98,39 @@ def test_cpp_host_programs(program, tmp_path):
     r = subprocess.run([exe], cwd=tmp_path, capture_output=True, text=True, timeout=300)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_vector_file_known_answers(tmp_path):
+    # the reference's fvecs case (test_cpu.cpp:117-135): rows r*10 + j, d=4, at most 2 rows read
+    rows = (np.arange(3)[:, None] * 10 + np.arange(4)[None, :]).astype(np.float32)
+    p = str(tmp_path / "t.fvecs")
+    host.write_fvecs(p, rows)
+    raw = np.fromfile(p, dtype="<i4")
+    assert raw.size == 15 and (raw[::5] == 4).all()  # int32 dimension before each row
+    got = host.read_fvecs(p, max_n=2)
+    assert got.shape == (2, 4) and got.ravel()[4] == 10.0 and got.ravel()[7] == 13.0
+    ids = np.array([[0, 1, 2], [100, 101, 102]], dtype=np.int32)
+    host.write_ivecs(str(tmp_path / "t.ivecs"), ids)
+    assert (host.read_ivecs(str(tmp_path / "t.ivecs")) == ids).all()
+    host.write_bvecs(str(tmp_path / "t.bvecs"), np.array([[7, 250]], dtype=np.uint8))
+    b = host.read_bvecs(str(tmp_path / "t.bvecs"))
+    assert b.dtype == np.float32 and b.tolist() == [[7.0, 250.0]]
+
+
+def test_vector_file_errors(tmp_path):
+    p = str(tmp_path / "bad.fvecs")
+    host.write_fvecs(p, np.ones((2, 3), np.float32))
+    with open(p, "ab") as f:
+        f.write(b"\x00\x00")  # a truncated third row
+    with pytest.raises(ValueError):
+        host.read_fvecs(p)
+    q = str(tmp_path / "mixed.fvecs")
+    with open(q, "wb") as f:
+        np.array([2], "<i4").tofile(f)
+        np.ones(2, "<f4").tofile(f)
+        np.array([1], "<i4").tofile(f)
+        np.ones(2, "<f4").tofile(f)  # second row claims d=1 but the byte count matches two rows of d=2
+    with pytest.raises(ValueError):
+        host.read_fvecs(q)
+    with pytest.raises(FileNotFoundError):
+        host.read_fvecs(str(tmp_path / "missing.fvecs"))

@@ -147,3 +147,54 @@ def recall_at_k(found: np.ndarray, truth_ids: np.ndarray, k: int) -> float:
     if r < 0:
         raise RuntimeError(library().vkh_last_error().decode())
     return r
+
+
+# ---- vector files (the TEXMEX formats of SIFT1M/GIST1M; reference src/cpu/io.cpp:12-52, C++ in host/io.cpp).
+# Each row is a little-endian int32 dimension followed by that many values: float32 (.fvecs), uint8 (.bvecs) or
+# int32 (.ivecs). The readers memory-map the file, check that every row carries the same dimension, and return at
+# most max_n rows (0 = all); .bvecs rows come back as float32 like the C++ reader's.
+
+def _read_vecs(path: str, value: np.dtype, max_n: int) -> np.ndarray:
+    raw = np.memmap(path, dtype=np.uint8, mode="r")
+    if raw.size < 4:
+        raise ValueError(f"{path}: empty or truncated vector file")
+    d = int(raw[:4].view("<i4")[0])
+    row = 4 + d * np.dtype(value).itemsize
+    if d <= 0 or raw.size % row:
+        raise ValueError(f"{path}: size {raw.size} is not a whole number of rows of dimension {d}")
+    n = raw.size // row if max_n == 0 else min(max_n, raw.size // row)
+    rows = raw[: n * row].reshape(n, row)
+    if (rows[:, :4].copy().view("<i4")[:, 0] != d).any():
+        raise ValueError(f"{path}: rows of differing dimension")
+    return np.ascontiguousarray(rows[:, 4:]).view(np.dtype(value).newbyteorder("<")).reshape(n, d)
+
+
+def read_fvecs(path: str, max_n: int = 0) -> np.ndarray:
+    return _read_vecs(path, np.float32, max_n).astype(np.float32, copy=False)
+
+
+def read_bvecs(path: str, max_n: int = 0) -> np.ndarray:
+    return _read_vecs(path, np.uint8, max_n).astype(np.float32)
+
+
+def read_ivecs(path: str, max_n: int = 0) -> np.ndarray:
+    return _read_vecs(path, np.int32, max_n).astype(np.int32, copy=False)
+
+
+def _write_vecs(path: str, x: np.ndarray, value: np.dtype) -> None:
+    x = np.ascontiguousarray(x, dtype=np.dtype(value).newbyteorder("<"))
+    n, d = x.shape
+    head = np.full((n, 1), d, dtype="<i4").view(np.uint8)
+    np.concatenate([head, x.view(np.uint8).reshape(n, -1)], axis=1).tofile(path)
+
+
+def write_fvecs(path: str, x: np.ndarray) -> None:
+    _write_vecs(path, x, np.float32)
+
+
+def write_bvecs(path: str, x: np.ndarray) -> None:
+    _write_vecs(path, x, np.uint8)
+
+
+def write_ivecs(path: str, x: np.ndarray) -> None:
+    _write_vecs(path, x, np.int32)
