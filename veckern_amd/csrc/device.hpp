@@ -39,6 +39,27 @@ __device__ __forceinline__ float wave_shr1(float v) {
 }
 __device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgcn_update_dpp(v, v, 0x138, 0xf, 0xf, false); }
 
+// Compare-exchange of a lane's pair with the pair of lane ^ j: the lane keeps the smaller of the two under the
+// (dist, id) order when keep_min, else the larger. Both lanes of an exchange decide consistently, so the two pairs
+// are kept, never duplicated (identical pairs, i.e. empty slots, may swap harmlessly).
+__device__ __forceinline__ void exchange_xor(float& d, int32_t& i, int j, bool keep_min) {
+    const float pd = __shfl_xor(d, j);
+    const int32_t pi = __shfl_xor(i, j);
+    if (pair_less(pd, pi, d, i) == keep_min) {
+        d = pd;
+        i = pi;
+    }
+}
+
+// Bitonic sort of one pair per lane, ascending by lane (21 compare-exchange steps).
+__device__ __forceinline__ void wave_sort(float& d, int32_t& i) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int k = 2; k <= WAVE; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) exchange_xor(d, i, j, ((lane & j) == 0) == ((lane & k) == 0 || k == WAVE));
+}
+
 // One sorted list of up to 64*S (dist, id) pairs spread over a wave: entry p lives in lane p % 64, register
 // p / 64. The admission threshold (entry K-1) is wave-uniform, so the compiler keeps it in SGPRs. Every
 // member must be called by all 64 lanes with wave-uniform arguments (control flow stays uniform).
@@ -46,7 +67,7 @@ __device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgc
 // `cap` is an optional outside bound: the threshold of another list over a disjoint part of the same candidate
 // stream (a sibling wave's). A candidate farther than it has K better candidates in that list, so it cannot be in
 // the merged top K and is not offered; ties at the cap are still offered, which keeps the (dist, id) order exact.
-template <int S>
+template <int S, bool BULK = (S > 1)>
 struct WaveList {
     float d[S];
     int32_t id[S];
@@ -128,9 +149,9 @@ struct WaveList {
         filter = fminf(thr_d, cap);
     }
 
-    // Each lane offers one candidate; admitted ones are inserted one at a time, lowest lane first. The ballot
-    // uses dist <= threshold as a cheap superset test; the exact (dist, id) test is re-done per candidate
-    // because the threshold falls as candidates go in.
+    // Each lane offers one candidate. The ballot uses dist <= threshold as a cheap superset test. A few admitted
+    // lanes are inserted one at a time, lowest lane first, with the exact (dist, id) test re-done per candidate
+    // because the threshold falls as candidates go in; kMergeMin or more go in by one bitonic merge.
     __device__ __forceinline__ void offer(float x, int32_t xi, bool valid, int K) {
         offer_masked(x, xi, __builtin_amdgcn_ballot_w64(valid), K);
     }
@@ -139,6 +160,10 @@ struct WaveList {
     // one compare into a scalar mask and one branch.
     __device__ __forceinline__ void offer_masked(float x, int32_t xi, uint64_t valid, int K) {
         uint64_t mask = __builtin_amdgcn_ballot_w64(x <= filter) & valid;
+        if (BULK && __popcll(mask) >= kMergeMin) {
+            merge_wave(x, xi, (mask >> __lane_id()) & 1, K);
+            return;
+        }
         while (mask) {
             const int src = __ffsll(static_cast<unsigned long long>(mask)) - 1;
             mask &= mask - 1;
@@ -146,6 +171,45 @@ struct WaveList {
             const int32_t vi = lane_read(xi, src);
             if (pair_less(vx, vi, thr_d, thr_i)) insert(vx, vi, K);
         }
+    }
+
+    // Admitted lanes from which one bitonic merge of the whole wave costs less than inserting them one by one.
+    // BULK = false inserts one by one always: by default for single-register lists (K <= 64), where the merge's
+    // code and registers cost the scan loop more than the inserts it replaces.
+    static constexpr int kMergeMin = 8;
+
+    // Admits every offered lane's pair at once: the wave's pairs are sorted (lanes not offering carry the empty
+    // slot), reversed, and folded into the list's last register by elementwise minimum, which leaves the list a
+    // bitonic sequence holding the 64*S smallest pairs of both; a bitonic clean sorts it. The result is the list
+    // the one-by-one inserts would give.
+    __device__ __forceinline__ void merge_wave(float x, int32_t xi, bool offered, int K) {
+        const int lane = __lane_id();
+        float cd = offered ? x : INFINITY;
+        int32_t ci = offered ? xi : kEmptyId;
+        wave_sort(cd, ci);
+        const float rd = __shfl(cd, WAVE - 1 - lane);
+        const int32_t ri = __shfl(ci, WAVE - 1 - lane);
+        if (pair_less(rd, ri, d[S - 1], id[S - 1])) {
+            d[S - 1] = rd;
+            id[S - 1] = ri;
+        }
+#pragma unroll
+        for (int h = S / 2; h > 0; h >>= 1)  // register distances (S is a power of two)
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+                if ((s & h) == 0 && pair_less(d[s + h], id[s + h], d[s], id[s])) {
+                    const float td = d[s];
+                    const int32_t ti = id[s];
+                    d[s] = d[s + h];
+                    id[s] = id[s + h];
+                    d[s + h] = td;
+                    id[s + h] = ti;
+                }
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int j = WAVE / 2; j > 0; j >>= 1) exchange_xor(d[s], id[s], j, (lane & j) == 0);
+        refresh(K);
     }
 
     // Writes entries 0..K-1 to dst (LDS or global).

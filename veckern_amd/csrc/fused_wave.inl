@@ -471,7 +471,9 @@ __global__ void __launch_bounds__(T)
 
         // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so the
         // scan loop offers every slot without a per-query test.
-        WaveList<S> lists[QS];
+        // Bulk merges (device.hpp) only for long lists: for K <= 64 their registers cost more than they save, and
+        // the fp16 kernels (Q = 8) have none to spare.
+        WaveList<S, !F16 && (S > 1)> lists[QS];
 #pragma unroll
         for (int q = 0; q < QS; ++q) {
             lists[q].init();
