@@ -39,25 +39,68 @@ __device__ __forceinline__ float wave_shr1(float v) {
 }
 __device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgcn_update_dpp(v, v, 0x138, 0xf, 0xf, false); }
 
-// Compare-exchange of a lane's pair with the pair of lane ^ j: the lane keeps the smaller of the two under the
-// (dist, id) order when keep_min, else the larger. Both lanes of an exchange decide consistently, so the two pairs
-// are kept, never duplicated (identical pairs, i.e. empty slots, may swap harmlessly).
-__device__ __forceinline__ void exchange_xor(float& d, int32_t& i, int j, bool keep_min) {
-    const float pd = __shfl_xor(d, j);
-    const int32_t pi = __shfl_xor(i, j);
-    if (pair_less(pd, pi, d, i) == keep_min) {
-        d = pd;
-        i = pi;
+// The value of lane ^ J. Within a row of 16 lanes by DPP (VALU only): quad_perm for J = 1, 2; for J = 4, 8 a
+// row_shl:J into the lanes whose bit J is clear and a row_shr:J into the others, selected by bank (4-lane group)
+// masks. J = 16 by ds_swizzle's bit-mask mode (xor within 32 lanes, no address), J = 32 by ds_bpermute.
+template <int J>
+__device__ __forceinline__ int xor_lane(int v) {
+    if constexpr (J == 1) {
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, false);  // quad_perm [1, 0, 3, 2]
+    } else if constexpr (J == 2) {
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, false);  // quad_perm [2, 3, 0, 1]
+    } else if constexpr (J == 4) {
+        const int t = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xf, 0x5, false);  // row_shl:4, banks 0, 2
+        return __builtin_amdgcn_update_dpp(t, v, 0x114, 0xf, 0xa, false);         // row_shr:4, banks 1, 3
+    } else if constexpr (J == 8) {
+        const int t = __builtin_amdgcn_update_dpp(v, v, 0x108, 0xf, 0x3, false);  // row_shl:8, banks 0, 1
+        return __builtin_amdgcn_update_dpp(t, v, 0x118, 0xf, 0xc, false);         // row_shr:8, banks 2, 3
+    } else if constexpr (J == 16) {
+        return __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1f);  // and 0x1f, or 0, xor 16
+    } else {
+        static_assert(J == 32, "lane distance");
+        return __builtin_amdgcn_ds_bpermute((__lane_id() ^ 32) << 2, v);
     }
 }
 
-// Bitonic sort of one pair per lane, ascending by lane (21 compare-exchange steps).
+// Compare-exchange of a lane's pair with the pair of lane ^ J: the lane keeps the smaller of the two under the
+// (dist, id) order when keep_min, else the larger. Both lanes of an exchange decide consistently, so the two pairs
+// are kept, never duplicated (identical pairs, i.e. empty slots, may swap harmlessly). Branch-free: the order test
+// uses non-short-circuit operators so that it becomes compares and selects.
+template <int J>
+__device__ __forceinline__ void exchange_xor(float& d, int32_t& i, bool keep_min) {
+    const float pd = __int_as_float(xor_lane<J>(__float_as_int(d)));
+    const int32_t pi = xor_lane<J>(i);
+    const bool less = (pd < d) | ((pd == d) & (pi < i));
+    const bool take = less == keep_min;
+    d = take ? pd : d;
+    i = take ? pi : i;
+}
+
+// Bitonic sort of one pair per lane, ascending by lane, or descending with DESC (21 compare-exchange steps).
+template <int K = 2, bool DESC = false>
 __device__ __forceinline__ void wave_sort(float& d, int32_t& i) {
+    if constexpr (K <= WAVE) {
+        const int lane = __lane_id();
+        const bool up = K == WAVE ? !DESC : (lane & K) == 0;
+        if constexpr (K >= 64) exchange_xor<32>(d, i, ((lane & 32) == 0) == up);
+        if constexpr (K >= 32) exchange_xor<16>(d, i, ((lane & 16) == 0) == up);
+        if constexpr (K >= 16) exchange_xor<8>(d, i, ((lane & 8) == 0) == up);
+        if constexpr (K >= 8) exchange_xor<4>(d, i, ((lane & 4) == 0) == up);
+        if constexpr (K >= 4) exchange_xor<2>(d, i, ((lane & 2) == 0) == up);
+        exchange_xor<1>(d, i, ((lane & 1) == 0) == up);
+        wave_sort<K * 2, DESC>(d, i);
+    }
+}
+
+// Sorts a bitonic sequence of one pair per lane ascending (6 compare-exchange steps).
+__device__ __forceinline__ void wave_clean(float& d, int32_t& i) {
     const int lane = __lane_id();
-#pragma unroll
-    for (int k = 2; k <= WAVE; k <<= 1)
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) exchange_xor(d, i, j, ((lane & j) == 0) == ((lane & k) == 0 || k == WAVE));
+    exchange_xor<32>(d, i, (lane & 32) == 0);
+    exchange_xor<16>(d, i, (lane & 16) == 0);
+    exchange_xor<8>(d, i, (lane & 8) == 0);
+    exchange_xor<4>(d, i, (lane & 4) == 0);
+    exchange_xor<2>(d, i, (lane & 2) == 0);
+    exchange_xor<1>(d, i, (lane & 1) == 0);
 }
 
 // One sorted list of up to 64*S (dist, id) pairs spread over a wave: entry p lives in lane p % 64, register
@@ -178,37 +221,32 @@ struct WaveList {
     // code and registers cost the scan loop more than the inserts it replaces.
     static constexpr int kMergeMin = 8;
 
-    // Admits every offered lane's pair at once: the wave's pairs are sorted (lanes not offering carry the empty
-    // slot), reversed, and folded into the list's last register by elementwise minimum, which leaves the list a
+    // Admits every offered lane's pair at once: the wave's pairs are sorted descending (lanes not offering carry
+    // the empty slot) and folded into the list's last register by elementwise minimum, which leaves the list a
     // bitonic sequence holding the 64*S smallest pairs of both; a bitonic clean sorts it. The result is the list
     // the one-by-one inserts would give.
     __device__ __forceinline__ void merge_wave(float x, int32_t xi, bool offered, int K) {
-        const int lane = __lane_id();
         float cd = offered ? x : INFINITY;
         int32_t ci = offered ? xi : kEmptyId;
-        wave_sort(cd, ci);
-        const float rd = __shfl(cd, WAVE - 1 - lane);
-        const int32_t ri = __shfl(ci, WAVE - 1 - lane);
-        if (pair_less(rd, ri, d[S - 1], id[S - 1])) {
-            d[S - 1] = rd;
-            id[S - 1] = ri;
-        }
+        wave_sort<2, true>(cd, ci);
+        const bool less = (cd < d[S - 1]) | ((cd == d[S - 1]) & (ci < id[S - 1]));
+        d[S - 1] = less ? cd : d[S - 1];
+        id[S - 1] = less ? ci : id[S - 1];
 #pragma unroll
         for (int h = S / 2; h > 0; h >>= 1)  // register distances (S is a power of two)
 #pragma unroll
             for (int s = 0; s < S; ++s)
-                if ((s & h) == 0 && pair_less(d[s + h], id[s + h], d[s], id[s])) {
-                    const float td = d[s];
-                    const int32_t ti = id[s];
-                    d[s] = d[s + h];
-                    id[s] = id[s + h];
-                    d[s + h] = td;
-                    id[s + h] = ti;
+                if ((s & h) == 0) {
+                    const bool swap = (d[s + h] < d[s]) | ((d[s + h] == d[s]) & (id[s + h] < id[s]));
+                    const float lo_d = swap ? d[s + h] : d[s], hi_d = swap ? d[s] : d[s + h];
+                    const int32_t lo_i = swap ? id[s + h] : id[s], hi_i = swap ? id[s] : id[s + h];
+                    d[s] = lo_d;
+                    id[s] = lo_i;
+                    d[s + h] = hi_d;
+                    id[s + h] = hi_i;
                 }
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int j = WAVE / 2; j > 0; j >>= 1) exchange_xor(d[s], id[s], j, (lane & j) == 0);
+        for (int s = 0; s < S; ++s) wave_clean(d[s], id[s]);
         refresh(K);
     }
 
