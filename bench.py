@@ -149,7 +149,6 @@ def bench_ivf(args, centroids, codes, queries, base):
     list_ids = vk.ivf_assign(coarse, base)
     log(f"[bench] IVF: {nlist} lists built in {time.time() - t0:.1f} s; largest list {np.bincount(list_ids).max()}")
     ix = vk.IVFIndex(coarse, centroids, codes, list_ids)
-    ix.set_tuning(vk.Tuning(queries_per_block=min(args.queries_per_block, 4)))
     # vectors each query's probed lists hold (coarse distances as float64 on the host: only the sizes are used)
     sizes = np.bincount(list_ids, minlength=nlist)
     cd = ((queries.astype(np.float64)[:, None, :] - coarse.astype(np.float64)[None]) ** 2).sum(-1)

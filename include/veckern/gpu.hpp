@@ -101,7 +101,7 @@ public:
     IVFSearcher& operator=(const IVFSearcher&) = delete;
 
     Timings search(const float* queries, std::size_t nq, std::size_t nprobe, std::size_t k, Neighbor* out);
-    void set_tuning(const Tuning& tuning);  // queries_per_block (1, 2 or 4) is the field that applies
+    void set_tuning(const Tuning& tuning);  // validated and kept; the scan takes one query per slab
 
 private:
     struct Impl;

@@ -181,7 +181,8 @@ void vk_ivf_destroy(vk_ivf* index);
 /* Index building helper: list_ids[i] = the coarse centroid nearest to x_i (exact squared L2, the lower index on
  * ties; 0 if every distance is NaN). coarse: nlist x d, x: n x d host buffers. */
 int vk_ivf_assign(const float* coarse, size_t nlist, size_t d, const float* x, size_t n, int32_t* list_ids);
-/* Queries per slab (queries_per_block, capped at 4) is the tuning field that applies; default 4. */
+/* The IVF scan takes one query per slab (a query's probed lists are scanned as one run); the tuning is validated
+ * and kept, and no field of it changes the launch. */
 int vk_ivf_set_tuning(vk_ivf* index, const vk_tuning* t);
 int vk_ivf_last_launch(const vk_ivf* index, vk_launch_shape* out);
 int vk_ivf_search(vk_ivf* index, const float* queries, size_t nq, size_t nprobe, size_t k, vk_neighbor* out,

@@ -1,8 +1,8 @@
 """GPU inverted-file search (vk_ivf_*) against the oracle's restatement (vko_ivf_search), bit-exact: coarse probe
 by exact distances (ties to the lower list id), then the exhaustive search's ADC distances and (dist, id) order
 over the probed lists only. Covers nprobe = 1 .. nlist (all lists = the exhaustive search), every K template,
-every queries-per-slab setting, empty and tiny lists, lists that span many blocks (one query), tie-heavy data and
-a run-time m.
+empty and tiny lists, a query whose lists span many blocks, blocks that finish many queries, tie-heavy data and a
+run-time m.
 """
 import numpy as np
 import pytest
@@ -56,12 +56,23 @@ def test_ivf_all_lists_is_the_exhaustive_search(index_case):
 
 
 @pytest.mark.parametrize("q", [1, 2, 4])
-def test_ivf_every_queries_per_slab(index_case, q):
+def test_ivf_takes_one_query_per_slab_whatever_the_tuning(index_case, q):
     (coarse, cent, codes, list_ids, queries), ix = index_case
     ix.set_tuning(vk.Tuning(queries_per_block=q))
     d, i, _ = ix.search(queries, 8, 33)
     assert_same(d, i, orc.ivf_search(coarse, cent, 64, codes, list_ids, queries, 8, 33), f"Q={q}")
-    assert ix.last_launch().queries_per_block == q
+    assert ix.last_launch().queries_per_block == 1
+
+
+def test_ivf_blocks_finish_many_queries():
+    # ~100 vectors per list (one granule each), 3000 queries x 2 probes: each block's range holds the runs of
+    # several queries, so lists are written and restarted inside a block; k = 100 exercises the long lists
+    coarse, cent, codes, list_ids, queries = ivf_case(96, 20_000, 32, 16, 3_000, 200)
+    with vk.IVFIndex(coarse, cent, codes, list_ids) as ix:
+        for k in (10, 100):
+            d, i, _ = ix.search(queries, 2, k)
+            assert_same(d, i, orc.ivf_search(coarse, cent, 32, codes, list_ids, queries, 2, k), f"k={k}")
+            assert ix.last_launch().blocks_x < 3_000 * 2
 
 
 def test_ivf_single_query_spreads_lists_over_many_blocks(index_case):

@@ -803,7 +803,7 @@ struct vk_ivf {
     DeviceBuffer<float> coarse, centroids, queries, lut;
     DeviceBuffer<uint4> codes_v;
     DeviceBuffer<int32_t> ids, slab_list, slab_queries, seg_len;
-    DeviceBuffer<int64_t> list_tile, slab_gran, part_offset, seg_off;
+    DeviceBuffer<int64_t> list_tile, slab_gran, query_gran, part_offset;
     DeviceBuffer<Pair> probes, part, out;
     DeviceBuffer<unsigned> error;
     std::vector<int64_t> list_tile_h;  // [nlist + 1]
@@ -847,117 +847,87 @@ struct vk_ivf {
                               stream));
         clock.settle();
 
-        // 2. slabs: for each list, the queries probing it in groups of up to Q (lists of exactly k entries)
+        // 2. slabs in query-major order: each query's probed lists in probe order, empty lists skipped, so a
+        // query's slabs are one run of consecutive granules
         const int K = static_cast<int>(kk);
         const int segments = K <= vk::WAVE ? 1 : 2;
-        const int q = std::min(4, vk::plan::cap_q_by_batch(
-                                      vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block,
-                                                            false, K), nq));
-        const vk::WaveScanKernel kern = vk::ivf_kernel(q, static_cast<int>(m), segments);
-        if (!kern.fn) fail(VK_ERR_LOGIC, "no IVF kernel built for this (Q, m, K)");
+        const vk::WaveScanKernel kern = vk::ivf_kernel(static_cast<int>(m), segments);
+        if (!kern.fn) fail(VK_ERR_LOGIC, "no IVF kernel built for this (m, K)");
         const int W = kern.threads / vk::WAVE;
-        std::vector<int64_t> per_list(nlist + 1, 0);
-        for (const Pair& p : probe_h)
-            if (p.i >= 0) ++per_list[p.i + 1];  // a query whose distances are all NaN probes nothing
-        for (size_t l = 0; l < nlist; ++l) per_list[l + 1] += per_list[l];
-        std::vector<int32_t> by_list(probe_h.size());  // (query, probe) pairs ordered by list, then query
-        {
-            std::vector<int64_t> fill(per_list.begin(), per_list.end() - 1);
-            for (size_t i = 0; i < probe_h.size(); ++i)
-                if (probe_h[i].i >= 0) by_list[fill[probe_h[i].i]++] = static_cast<int32_t>(i);
-        }
-        std::vector<int32_t> s_list, s_queries;
-        std::vector<int64_t> s_gran{0};
-        std::vector<int64_t> pair_slab(probe_h.size(), -1);  // slab and slot of every (query, probe)
-        std::vector<int32_t> pair_pos(probe_h.size(), 0);
-        for (size_t l = 0; l < nlist; ++l) {
-            const int64_t tiles = list_tile_h[l + 1] - list_tile_h[l];
-            if (tiles == 0) continue;  // an empty list contributes nothing
-            for (int64_t j = per_list[l]; j < per_list[l + 1]; j += q) {
-                const int64_t slab = static_cast<int64_t>(s_list.size());
-                s_list.push_back(static_cast<int32_t>(l));
-                for (int u = 0; u < q; ++u) {
-                    const int64_t jj = j + u;
-                    if (jj < per_list[l + 1]) {
-                        const int32_t pr = by_list[jj];
-                        s_queries.push_back(pr / static_cast<int32_t>(nprobe));
-                        pair_slab[pr] = slab;
-                        pair_pos[pr] = u;
-                    } else {
-                        s_queries.push_back(-1);
-                    }
-                }
+        std::vector<int32_t> s_list, s_query;
+        std::vector<int64_t> s_gran{0}, q_gran(nq + 1, 0);
+        s_list.reserve(probe_h.size());
+        s_query.reserve(probe_h.size());
+        s_gran.reserve(probe_h.size() + 1);
+        for (size_t qi = 0; qi < nq; ++qi) {
+            q_gran[qi] = s_gran.back();
+            for (size_t p = 0; p < nprobe; ++p) {
+                const int32_t l = probe_h[qi * nprobe + p].i;
+                if (l < 0) continue;  // a query whose distances are all NaN probes nothing
+                const int64_t tiles = list_tile_h[l + 1] - list_tile_h[l];
+                if (tiles == 0) continue;  // an empty list contributes nothing
+                s_list.push_back(l);
+                s_query.push_back(static_cast<int32_t>(qi));
                 s_gran.push_back(s_gran.back() + tiles / 4);
             }
         }
+        q_gran[nq] = s_gran.back();
         const int64_t n_slabs = static_cast<int64_t>(s_list.size());
         const int64_t total = s_gran.back();
 
-        // 3. balanced partition of all granules, partial-list offsets, and each query's merge segments
+        // 3. balanced partition of all granules and each query's partial lists: one per wave of every block that
+        // covers the query's run
         int per_cu = 0;
-        const size_t smem = kern.dynamic_lds ? static_cast<size_t>(q) * m * vk::KSUB * sizeof(float) : 0;
+        const size_t smem = kern.dynamic_lds ? m * vk::KSUB * sizeof(float) : 0;
         if (kern.dynamic_lds)
             VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
         VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
         per_cu = std::max(per_cu, 1);
         const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(per_cu) * info.sm_count,
                                                                       total));
-        std::vector<int32_t> count(n_slabs);
-        int max_count = 0;
-        for (int64_t s = 0; s < n_slabs; ++s) {
-            const int64_t lo = vk::first_block_of(s_gran[s], grid, total);
-            count[s] = static_cast<int32_t>(vk::first_block_of(s_gran[s + 1] - 1, grid, total) - lo + 1);
-            max_count = std::max(max_count, count[s]);
-        }
-        const int lpb = max_count > 8 ? 1 : W;
-        std::vector<int64_t> p_off(n_slabs);
+        std::vector<int64_t> p_off(nq);
+        std::vector<int32_t> p_len(nq);
         int64_t pairs = 0;
-        for (int64_t s = 0; s < n_slabs; ++s) {
-            p_off[s] = pairs;
-            pairs += static_cast<int64_t>(q) * count[s] * lpb * K;
-        }
-        std::vector<int64_t> g_off(probe_h.size(), 0);
-        std::vector<int32_t> g_len(probe_h.size(), 0);
-        for (size_t i = 0; i < probe_h.size(); ++i) {
-            const int64_t s = pair_slab[i];
-            if (s < 0) continue;
-            const int64_t per_query = static_cast<int64_t>(count[s]) * lpb * K;
-            g_off[i] = p_off[s] + pair_pos[i] * per_query;
-            g_len[i] = static_cast<int32_t>(per_query);
+        for (size_t qi = 0; qi < nq; ++qi) {
+            int64_t count = 0;
+            if (q_gran[qi + 1] > q_gran[qi])
+                count = vk::first_block_of(q_gran[qi + 1] - 1, grid, total) -
+                        vk::first_block_of(q_gran[qi], grid, total) + 1;
+            p_off[qi] = pairs;
+            p_len[qi] = static_cast<int32_t>(count * W * K);
+            pairs += count * W * K;
         }
 
         last = vk_launch_shape{};
         last.threads = kern.threads;
         last.blocks_x = static_cast<int>(grid);
         last.grid_y = 1;
-        last.queries_per_block = q;
+        last.queries_per_block = 1;
         last.vectors_per_step = 4;
         last.blocks_per_sm = per_cu;
         last.waves = static_cast<double>(grid) / (static_cast<double>(per_cu) * info.sm_count);
 
         part.ensure(static_cast<size_t>(std::max<int64_t>(pairs, 1)));
-        seg_off.ensure(g_off.size());
-        seg_len.ensure(g_len.size());
-        if (n_slabs > 0) {
-            slab_list.ensure(s_list.size());
-            slab_queries.ensure(s_queries.size());
-            slab_gran.ensure(s_gran.size());
-            part_offset.ensure(p_off.size());
-            clock.time(&t->transfer_ms, [&] {
+        part_offset.ensure(nq);
+        seg_len.ensure(nq);
+        query_gran.ensure(nq + 1);
+        clock.time(&t->transfer_ms, [&] {
+            if (n_slabs > 0) {
+                slab_list.ensure(s_list.size());
+                slab_queries.ensure(s_query.size());
+                slab_gran.ensure(s_gran.size());
                 VK_HIP(hipMemcpyAsync(slab_list.get(), s_list.data(), s_list.size() * sizeof(int32_t),
                                       hipMemcpyHostToDevice, stream));
-                VK_HIP(hipMemcpyAsync(slab_queries.get(), s_queries.data(), s_queries.size() * sizeof(int32_t),
+                VK_HIP(hipMemcpyAsync(slab_queries.get(), s_query.data(), s_query.size() * sizeof(int32_t),
                                       hipMemcpyHostToDevice, stream));
                 VK_HIP(hipMemcpyAsync(slab_gran.get(), s_gran.data(), s_gran.size() * sizeof(int64_t),
                                       hipMemcpyHostToDevice, stream));
-                VK_HIP(hipMemcpyAsync(part_offset.get(), p_off.data(), p_off.size() * sizeof(int64_t),
-                                      hipMemcpyHostToDevice, stream));
-            });
-        }
-        clock.time(&t->transfer_ms, [&] {
-            VK_HIP(hipMemcpyAsync(seg_off.get(), g_off.data(), g_off.size() * sizeof(int64_t), hipMemcpyHostToDevice,
-                                  stream));
-            VK_HIP(hipMemcpyAsync(seg_len.get(), g_len.data(), g_len.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+            }
+            VK_HIP(hipMemcpyAsync(query_gran.get(), q_gran.data(), q_gran.size() * sizeof(int64_t),
+                                  hipMemcpyHostToDevice, stream));
+            VK_HIP(hipMemcpyAsync(part_offset.get(), p_off.data(), p_off.size() * sizeof(int64_t),
+                                  hipMemcpyHostToDevice, stream));
+            VK_HIP(hipMemcpyAsync(seg_len.get(), p_len.data(), p_len.size() * sizeof(int32_t), hipMemcpyHostToDevice,
                                   stream));
         });
 
@@ -974,20 +944,21 @@ struct vk_ivf {
             a.K = K;
             a.k = static_cast<int>(kk);
             a.total = total;
-            a.lists_per_block = lpb;
+            a.lists_per_block = W;
             a.part = part.get();
             a.n_slabs = n_slabs;
             a.slab_gran = slab_gran.get();
             a.slab_list = slab_list.get();
             a.slab_queries = slab_queries.get();
+            a.query_gran = query_gran.get();
             a.list_tile = list_tile.get();
             a.ids = ids.get();
             a.part_offset = part_offset.get();
             a.lut = lut.get();
             clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(grid), smem, stream)); });
         }
-        vk::IvfMergeArgs ma{part.get(), seg_off.get(), seg_len.get(), static_cast<int>(nprobe),
-                            static_cast<int64_t>(nq), K, static_cast<int>(kk), d_o};
+        vk::IvfMergeArgs ma{part.get(), part_offset.get(), seg_len.get(), static_cast<int64_t>(nq), K,
+                            static_cast<int>(kk), d_o};
         clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_ivf_merge(ma, stream)); });
     }
 };

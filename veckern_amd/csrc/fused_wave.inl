@@ -375,17 +375,20 @@ __device__ __forceinline__ int64_t slab_of(const int64_t* slab_gran, int64_t sla
     return lo;
 }
 
-// IVF: the scan runs over inverted lists. Slab s is list a.slab_list[s] for the queries a.slab_queries[s * QS ..]
-// (-1 pads; the first is always a real query), its granules are [a.slab_gran[s], a.slab_gran[s + 1]) of the
-// balanced partition, the list's padded tiles start at a.list_tile[list] in the word-interleaved codes, and the
-// vector ids come from a.ids (-1 on padding). Each (block, slab) writes its partial lists at a.part_offset[s];
-// a separate merge kernel combines a query's partial lists over all the lists it probed.
+// IVF (one query per slab, QS = 1): the scan runs over inverted lists. Slab s is list a.slab_list[s] probed by
+// query a.slab_queries[s]; slabs are in query-major order, so a query's probed lists form one run of consecutive
+// slabs, granules [a.query_gran[q], a.query_gran[q + 1]) of the balanced partition. Slab s covers granules
+// [a.slab_gran[s], a.slab_gran[s + 1]), its list's padded tiles start at a.list_tile[list] in the
+// word-interleaved codes, and the vector ids come from a.ids (-1 on padding). A block gathers a query's tables and
+// starts its lists once per run and writes them once, at the end of the run (or of its range); a separate merge
+// kernel combines the partial lists of each query.
 template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF>
 __global__ void __launch_bounds__(T)
     __attribute__((amdgpu_waves_per_eu(wave_kernel_waves_per_simd<QG, NG, M, T, F16>())))
     fused_wave_kernel_t(WaveScanArgs a) {
     constexpr int QS = QG * NG;
     constexpr int W = T / WAVE;
+    static_assert(!IVF || (QS == 1 && !F16), "inverted-list scans take one query per slab and fp32 tables");
     using E = Entries<QG, F16>;
     using V = typename E::T;
     // With m fixed the tables are a static LDS array at address 0, so a lookup address is one SDWA shift of
@@ -419,6 +422,13 @@ __global__ void __launch_bounds__(T)
     // (slabs are non-empty and contiguous in item order), so the search costs one chain of dependent loads per
     // block, not one per slab.
     int64_t next_slab = IVF && start < end ? slab_of(a.slab_gran, a.n_slabs, start) : 0;
+    // Bulk merges (device.hpp) for long lists, and for inverted lists, whose partial lists cover a few probed lists
+    // each, so that many of their candidates arrive while the list is filling. Elsewhere, for K <= 64, their
+    // registers cost more than they save, and the fp16 kernels (Q = 8) have none to spare.
+    WaveList<S, IVF || (!F16 && S > 1)> lists[QS];
+    float published[QS];
+    const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
+    int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
     for (int64_t item = start; item < end;) {
         // The slab holding `item` and its granules [slab_first, slab_next) in the balanced partition.
         int64_t slab, slab_first, slab_next;
@@ -434,56 +444,56 @@ __global__ void __launch_bounds__(T)
         const int64_t g_lo = item - slab_first;
         const int64_t g_hi = min(end, slab_next) - slab_first;
         // Query rows of the slab; live[q] is false for padded slots (which repeat a real query's row). lrow: the
-        // rows of the per-search tables (inverted lists).
+        // query's row of the per-search tables (inverted lists). An inverted-list slab continues the run of its
+        // query's slabs (query-major order) unless the query changes: tables and lists carry over.
         const float* qrow[QS];
         const float* lrow[QS];
         bool live[QS];
+        bool new_run = true;
+        if constexpr (IVF) {
+            const int32_t qi = a.slab_queries[slab];
+            new_run = qi != run_query;
+            run_query = qi;
+            qrow[0] = a.queries + static_cast<int64_t>(qi) * a.d;
+            lrow[0] = a.lut + static_cast<int64_t>(qi) * (M ? M : a.m) * KSUB;
+            live[0] = true;
+        } else {
 #pragma unroll
-        for (int q = 0; q < QS; ++q) {
-            int64_t qi;
-            if constexpr (IVF) {
-                qi = a.slab_queries[slab * QS + q];
-                live[q] = qi >= 0;
-                if (!live[q]) qi = a.slab_queries[slab * QS];
-            } else {
-                qi = slab * QS + q;
+            for (int q = 0; q < QS; ++q) {
+                int64_t qi = slab * QS + q;
                 live[q] = qi < a.nq;
                 if (!live[q]) qi = a.nq - 1;
+                qrow[q] = a.queries + qi * a.d;
+                lrow[q] = nullptr;
             }
-            qrow[q] = a.queries + qi * a.d;
-            lrow[q] = IVF ? a.lut + qi * (M ? M : a.m) * KSUB : nullptr;
         }
         int64_t list_tile0 = 0;  // IVF: first tile of the slab's list
         if constexpr (IVF) list_tile0 = a.list_tile[a.slab_list[slab]];
 
-        __syncthreads();  // the previous slab's merge has finished with LDS
-        if constexpr (F16) {
-            if (tid < QS) qmax[tid] = 0u;
+        if (new_run) {
+            __syncthreads();  // the previous slab's merge has finished with LDS
+            if constexpr (F16) {
+                if (tid < QS) qmax[tid] = 0u;
+                __syncthreads();
+                table_maxima<QS, M, W>(a, qrow, qmax, wave, lane);
+                __syncthreads();
+            }
+            if constexpr (IVF) gather_tables<QG, M, T>(a, lrow, tables, tid);
+            else build_tables<QG, NG, M, W, F16>(a, qrow, tables, table_bytes, qmax, wave, lane);
+            if constexpr (kShareBound)
+                for (int t = tid; t < QS * W; t += T) (&rank_bound[0][0])[t] = 0x7f800000u;  // +inf
             __syncthreads();
-            table_maxima<QS, M, W>(a, qrow, qmax, wave, lane);
-            __syncthreads();
-        }
-        if constexpr (IVF && !F16 && NG == 1) gather_tables<QG, M, T>(a, lrow, tables, tid);
-        else build_tables<QG, NG, M, W, F16>(a, qrow, tables, table_bytes, qmax, wave, lane);
-        if constexpr (kShareBound)
-            for (int t = tid; t < QS * W; t += T) (&rank_bound[0][0])[t] = 0x7f800000u;  // +inf
-        __syncthreads();
 
-        // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so the
-        // scan loop offers every slot without a per-query test.
-        // Bulk merges (device.hpp) only for long lists: for K <= 64 their registers cost more than they save, and
-        // the fp16 kernels (Q = 8) have none to spare.
-        WaveList<S, !F16 && (S > 1)> lists[QS];
+            // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so
+            // the scan loop offers every slot without a per-query test.
 #pragma unroll
-        for (int q = 0; q < QS; ++q) {
-            lists[q].init();
-            if (!live[q]) lists[q].disable();
+            for (int q = 0; q < QS; ++q) {
+                lists[q].init();
+                if (!live[q]) lists[q].disable();
+                published[q] = INFINITY;
+            }
         }
         const uint32_t n32 = static_cast<uint32_t>(a.n);  // n < 2^31: ids and tile bounds fit in 32 bits
-        const int bound_rank = (a.K + W - 1) / W - 1;      // < 64: the entry lives in the lists' first register
-        float published[QS];
-#pragma unroll
-        for (int q = 0; q < QS; ++q) published[q] = INFINITY;
 
         for (int64_t g = g_lo + wave; g < g_hi; g += W) {
             // The block's bound per query (a stale slot only loosens it: published values only fall).
@@ -509,6 +519,13 @@ __global__ void __launch_bounds__(T)
                 for (int u = 0; u < U; ++u)
 #pragma unroll
                     for (int w = 0; w < WORDS; ++w) cw[u][w] = tile_codes[(u * WORDS + w) * WAVE];
+            }
+            // Inverted lists: the tiles' vector ids travel with their codes (loaded after a tile's lookups, each
+            // would cost its own memory round trip behind the scheduling fence).
+            int32_t vids[IVF ? U : 1];
+            if constexpr (IVF) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) vids[u] = a.ids[(list_tile0 + tile0 + u) * WAVE + lane];
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -563,7 +580,7 @@ __global__ void __launch_bounds__(T)
                 uint32_t id;
                 uint64_t valid;
                 if constexpr (IVF) {
-                    const int32_t vid = a.ids[(list_tile0 + tile0 + u) * WAVE + lane];
+                    const int32_t vid = vids[u];
                     id = static_cast<uint32_t>(vid);
                     valid = __builtin_amdgcn_ballot_w64(vid >= 0);
                 } else {
@@ -587,6 +604,18 @@ __global__ void __launch_bounds__(T)
             }
         }
 
+        // Inverted lists: when the query's run of slabs ends (or the block's range does), every wave writes its
+        // list for the query at part[part_offset[query] + (slot * W + wave) * K], slot = this block's index among
+        // the blocks that cover the run; the merge kernel combines them.
+        if constexpr (IVF) {
+            item = slab_next;
+            if (item >= end || a.slab_queries[next_slab] != run_query) {  // next_slab < n_slabs when item < end
+                const int64_t lo = first_block_of(a.query_gran[run_query], grid, a.total);
+                lists[0].store(a.part + a.part_offset[run_query] + ((b - lo) * W + wave) * a.K, a.K);
+            }
+            continue;
+        }
+
         // Partial lists of this (block, slab): part[slab][q][slot][list][K], the lists of one query contiguous.
         // With few blocks per slab every wave writes its own lists; with many, the block first merges its W lists
         // per query in LDS (the tables are dead by then), so the final merge reads W times fewer pairs.
@@ -594,10 +623,8 @@ __global__ void __launch_bounds__(T)
         const int count = static_cast<int>(first_block_of(slab_next - 1, grid, a.total) - lo + 1);
         const int slot = static_cast<int>(b - lo);
         const int lpb = a.lists_per_block;
-        // Uniform slabs reserve max_slots blocks each; inverted-list slabs have their own offsets and counts.
-        const int slots = IVF ? count : a.max_slots;
-        Pair* const slab_part = IVF ? a.part + a.part_offset[slab]
-                                    : a.part + slab * QS * a.max_slots * lpb * static_cast<int64_t>(a.K);
+        const int slots = a.max_slots;  // every slab reserves max_slots blocks
+        Pair* const slab_part = a.part + slab * QS * a.max_slots * lpb * static_cast<int64_t>(a.K);
         Pair* const buf = reinterpret_cast<Pair*>(tables);  // QS * W * K pairs fit in the tables' space
         if (lpb == 1) {
             __syncthreads();  // every wave has finished reading the tables
@@ -617,10 +644,6 @@ __global__ void __launch_bounds__(T)
         // counter is incremented with wrap-around at count - 1, so it is back at zero for the next search. The
         // agent-scope release fence after the barrier publishes the whole block's partial lists before the
         // increment; the last block's acquire fence makes every other block's lists visible to it.
-        if constexpr (IVF) {  // the merge kernel finishes inverted-list searches
-            item = slab_next;
-            continue;
-        }
         __syncthreads();
         if (tid == 0) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -661,23 +684,12 @@ WaveScanKernel make_wave_kernel() {
     return k;
 }
 
-// Inverted-list instances for one M: fp32 tables, QG 1, 2, 4 in one group, four tiles per wave step (each list
-// is padded to a multiple of 256 vectors).
+// Inverted-list instances for one M: fp32 tables, one query per slab, four tiles per wave step (each list is
+// padded to a multiple of 256 vectors).
 template <int M>
-WaveScanKernel select_ivf_kernel(int qg, int segments) {
-    constexpr int kLds = 160 * 1024;
-#define VK_IVF_CASE(QG_)                                                                            \
-    if (qg == QG_) {                                                                                \
-        if constexpr (M == 0 || M * KSUB * Entries<QG_, false>::kBytes <= kLds) {                   \
-            if (segments == 1) return make_wave_kernel<QG_, 1, 4, M, 1, false, true>();             \
-            if (segments == 2) return make_wave_kernel<QG_, 1, 4, M, 2, false, true>();             \
-        }                                                                                           \
-        return WaveScanKernel{};                                                                    \
-    }
-    VK_IVF_CASE(1)
-    VK_IVF_CASE(2)
-    VK_IVF_CASE(4)
-#undef VK_IVF_CASE
+WaveScanKernel select_ivf_kernel(int segments) {
+    if (segments == 1) return make_wave_kernel<1, 1, 4, M, 1, false, true>();
+    if (segments == 2) return make_wave_kernel<1, 1, 4, M, 2, false, true>();
     return WaveScanKernel{};
 }
 

@@ -1,22 +1,22 @@
 // Inverted-file (IVF) search, the reference's "coarse partitioning" next step (README.md:219): per query, the
 // nprobe nearest coarse centroids (exact distances, the re-rank kernel with every list as a candidate), then the
-// fused wave-list scan over only those lists' PQ codes (fused_wave.inl with IVF = true, slabs = (list, up to Q
-// queries probing it)), then this file's merge of each query's partial lists over its probed lists.
+// fused wave-list scan over only those lists' PQ codes (fused_wave.inl with IVF = true: slabs = (query, probed
+// list) in query-major order), then this file's merge of each query's partial lists.
 #include "kernels.hpp"
 
 namespace vk {
 
-WaveScanKernel ivf_kernel_m16(int qg, int segments);
-WaveScanKernel ivf_kernel_m32(int qg, int segments);
-WaveScanKernel ivf_kernel_m64(int qg, int segments);
-WaveScanKernel ivf_kernel_mx(int qg, int segments);
+WaveScanKernel ivf_kernel_m16(int segments);
+WaveScanKernel ivf_kernel_m32(int segments);
+WaveScanKernel ivf_kernel_m64(int segments);
+WaveScanKernel ivf_kernel_mx(int segments);
 
-WaveScanKernel ivf_kernel(int qg, int m, int segments) {
+WaveScanKernel ivf_kernel(int m, int segments) {
     switch (m) {
-        case 16: return ivf_kernel_m16(qg, segments);
-        case 32: return ivf_kernel_m32(qg, segments);
-        case 64: return ivf_kernel_m64(qg, segments);
-        default: return ivf_kernel_mx(qg, segments);
+        case 16: return ivf_kernel_m16(segments);
+        case 32: return ivf_kernel_m32(segments);
+        case 64: return ivf_kernel_m64(segments);
+        default: return ivf_kernel_mx(segments);
     }
 }
 
@@ -24,8 +24,8 @@ namespace {
 
 constexpr int kMergeThreads = 256;
 
-// One wave per query streams the pairs of its partial-list segments through a wave list (four 64-pair chunks in
-// flight per round) and writes the k best, empty slots as {+inf, -1}.
+// One wave per query streams the pairs of its partial lists through a wave list (four 64-pair chunks in flight
+// per round) and writes the k best, empty slots as {+inf, -1}.
 template <int S>
 __global__ void __launch_bounds__(kMergeThreads) ivf_merge_kernel(IvfMergeArgs a) {
     const int lane = __lane_id();
@@ -34,20 +34,18 @@ __global__ void __launch_bounds__(kMergeThreads) ivf_merge_kernel(IvfMergeArgs a
     if (q >= a.nq) return;  // wave-uniform
     WaveList<S> wl;
     wl.init();
-    for (int p = 0; p < a.probes; ++p) {
-        const Pair* first = a.part + a.seg_off[q * a.probes + p];
-        const int len = a.seg_len[q * a.probes + p];
-        constexpr int B = 4;
-        for (int base = 0; base < len; base += B * WAVE) {
-            Pair e[B];
+    const Pair* first = a.part + a.seg_off[q];
+    const int len = a.seg_len[q];
+    constexpr int B = 4;
+    for (int base = 0; base < len; base += B * WAVE) {
+        Pair e[B];
 #pragma unroll
-            for (int u = 0; u < B; ++u) {
-                const int j = base + u * WAVE + lane;
-                e[u] = j < len ? first[j] : Pair{INFINITY, kEmptyId};
-            }
-#pragma unroll
-            for (int u = 0; u < B; ++u) wl.offer(e[u].d, e[u].i, e[u].i != kEmptyId, a.K);
+        for (int u = 0; u < B; ++u) {
+            const int j = base + u * WAVE + lane;
+            e[u] = j < len ? first[j] : Pair{INFINITY, kEmptyId};
         }
+#pragma unroll
+        for (int u = 0; u < B; ++u) wl.offer(e[u].d, e[u].i, e[u].i != kEmptyId, a.K);
     }
     Pair* out = a.out + q * a.k;
 #pragma unroll

@@ -2,5 +2,5 @@
 #include "fused_wave.inl"
 
 namespace vk {
-WaveScanKernel ivf_kernel_m16(int qg, int segments) { return select_ivf_kernel<16>(qg, segments); }
+WaveScanKernel ivf_kernel_m16(int segments) { return select_ivf_kernel<16>(segments); }
 }  // namespace vk

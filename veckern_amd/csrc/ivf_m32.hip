@@ -2,5 +2,5 @@
 #include "fused_wave.inl"
 
 namespace vk {
-WaveScanKernel ivf_kernel_m32(int qg, int segments) { return select_ivf_kernel<32>(qg, segments); }
+WaveScanKernel ivf_kernel_m32(int segments) { return select_ivf_kernel<32>(segments); }
 }  // namespace vk

@@ -2,5 +2,5 @@
 #include "fused_wave.inl"
 
 namespace vk {
-WaveScanKernel ivf_kernel_m64(int qg, int segments) { return select_ivf_kernel<64>(qg, segments); }
+WaveScanKernel ivf_kernel_m64(int segments) { return select_ivf_kernel<64>(segments); }
 }  // namespace vk

@@ -2,5 +2,5 @@
 #include "fused_wave.inl"
 
 namespace vk {
-WaveScanKernel ivf_kernel_mx(int qg, int segments) { return select_ivf_kernel<0>(qg, segments); }
+WaveScanKernel ivf_kernel_mx(int segments) { return select_ivf_kernel<0>(segments); }
 }  // namespace vk

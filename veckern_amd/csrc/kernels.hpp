@@ -40,14 +40,15 @@ struct WaveScanArgs {
     Pair* part;              // [slabs][qg * ng][max_slots][lists_per_block][K]
     unsigned* counters;      // [slabs], zero between searches: blocks of a slab that have finished
     Pair* out;               // [nq][k]; empty slots become {+inf, -1}
-    // Inverted lists (IVF instances only); `n_gran` and `max_slots` are then unused.
+    // Inverted lists (IVF instances only, one query per slab); `n_gran` and `max_slots` are then unused.
     int64_t n_slabs;
     const int64_t* slab_gran;      // [n_slabs + 1] granule prefix of the slabs
     const int32_t* slab_list;      // [n_slabs] list scanned by each slab
-    const int32_t* slab_queries;   // [n_slabs][qg] query of each slot, -1 for padding (slot 0 is always real)
+    const int32_t* slab_queries;   // [n_slabs] query of each slab; a query's slabs are consecutive
+    const int64_t* query_gran;     // [nq + 1] granule prefix of the queries' runs of slabs
     const int64_t* list_tile;      // [lists + 1] first tile of each list in `codes` / `ids`
     const int32_t* ids;            // [tiles * 64] vector id of each padded position, -1 for padding
-    const int64_t* part_offset;    // [n_slabs] first pair of each slab's partial lists in `part`
+    const int64_t* part_offset;    // [nq] first pair of each query's partial lists in `part`
     const float* lut;              // [nq][m][256] tables computed once per search (a query meets many lists)
 };
 
@@ -60,16 +61,15 @@ struct WaveScanKernel {
 
 // Returns a kernel with fn == nullptr when the combination is not built. f16: binary16 tables (v9).
 WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16);
-// The inverted-list scan (ivf_m*.hip): fp32 tables, QG queries per slab, four tiles per wave step.
-WaveScanKernel ivf_kernel(int qg, int m, int segments);
+// The inverted-list scan (ivf_m*.hip): fp32 tables, one query per slab, four tiles per wave step.
+WaveScanKernel ivf_kernel(int m, int segments);
 
-// ---- IVF final merge (ivf.hip): query q's partial lists are the segments seg_off[q * probes + p] .. + seg_len
-// (pairs) for p < probes; its k results go to out[q * k].
+// ---- IVF final merge (ivf.hip): query q's partial lists are the pairs part[seg_off[q] .. + seg_len[q]); its k
+// results go to out[q * k].
 struct IvfMergeArgs {
     const Pair* part;
     const int64_t* seg_off;
     const int32_t* seg_len;
-    int probes;
     int64_t nq;
     int K;
     int k;
