@@ -802,8 +802,8 @@ struct vk_ivf {
     hipStream_t stream = nullptr;
     DeviceBuffer<float> coarse, centroids, queries, lut;
     DeviceBuffer<uint4> codes_v;
-    DeviceBuffer<int32_t> ids, slab_list, slab_queries, seg_len;
-    DeviceBuffer<int64_t> list_tile, slab_gran, query_gran, part_offset;
+    DeviceBuffer<int32_t> ids, slab_list, slab_queries;
+    DeviceBuffer<int64_t> list_tile, slab_gran, query_gran;
     DeviceBuffer<Pair> probes, part, out;
     DeviceBuffer<unsigned> error;
     std::vector<int64_t> list_tile_h;  // [nlist + 1]
@@ -837,66 +837,38 @@ struct vk_ivf {
         pa.out = probes.get();
         pa.error = error.get();
         lut.ensure(nq * m * vk::KSUB);
+        // 2. the slab plan, on the device: slabs in query-major order (each query's probed lists in probe order),
+        // so a query's slabs are one run of consecutive granules
+        const size_t slabs = nq * nprobe;
+        slab_list.ensure(slabs);
+        slab_queries.ensure(slabs);
+        slab_gran.ensure(slabs + 1);
+        query_gran.ensure(nq + 1);
+        vk::IvfPlanArgs plan{probes.get(),      static_cast<int>(nprobe), static_cast<int64_t>(nq), list_tile.get(),
+                             slab_list.get(),   slab_queries.get(),       slab_gran.get(),           query_gran.get()};
         clock.time(&t->lut_ms, [&] {
             VK_HIP(vk::launch_rerank(pa, stream));
             VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(nq),
                                   1, static_cast<int>(nq), lut.get(), stream));
+            VK_HIP(vk::launch_ivf_plan(plan, stream));
         });
-        std::vector<Pair> probe_h(nq * nprobe);
-        VK_HIP(hipMemcpyAsync(probe_h.data(), probes.get(), probe_h.size() * sizeof(Pair), hipMemcpyDeviceToHost,
-                              stream));
-        clock.settle();
 
-        // 2. slabs in query-major order: each query's probed lists in probe order, empty lists skipped, so a
-        // query's slabs are one run of consecutive granules
+        // 3. the scan over the probed lists: a balanced partition of all granules over one wave of blocks (the
+        // total is known only on the device; blocks with an empty range return at once), then the per-query merge
+        // of the lists of the blocks that covered each query's run
         const int K = static_cast<int>(kk);
         const int segments = K <= vk::WAVE ? 1 : 2;
         const vk::WaveScanKernel kern = vk::ivf_kernel(static_cast<int>(m), segments);
         if (!kern.fn) fail(VK_ERR_LOGIC, "no IVF kernel built for this (m, K)");
         const int W = kern.threads / vk::WAVE;
-        std::vector<int32_t> s_list, s_query;
-        std::vector<int64_t> s_gran{0}, q_gran(nq + 1, 0);
-        s_list.reserve(probe_h.size());
-        s_query.reserve(probe_h.size());
-        s_gran.reserve(probe_h.size() + 1);
-        for (size_t qi = 0; qi < nq; ++qi) {
-            q_gran[qi] = s_gran.back();
-            for (size_t p = 0; p < nprobe; ++p) {
-                const int32_t l = probe_h[qi * nprobe + p].i;
-                if (l < 0) continue;  // a query whose distances are all NaN probes nothing
-                const int64_t tiles = list_tile_h[l + 1] - list_tile_h[l];
-                if (tiles == 0) continue;  // an empty list contributes nothing
-                s_list.push_back(l);
-                s_query.push_back(static_cast<int32_t>(qi));
-                s_gran.push_back(s_gran.back() + tiles / 4);
-            }
-        }
-        q_gran[nq] = s_gran.back();
-        const int64_t n_slabs = static_cast<int64_t>(s_list.size());
-        const int64_t total = s_gran.back();
-
-        // 3. balanced partition of all granules and each query's partial lists: one per wave of every block that
-        // covers the query's run
         int per_cu = 0;
         const size_t smem = kern.dynamic_lds ? m * vk::KSUB * sizeof(float) : 0;
         if (kern.dynamic_lds)
             VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
         VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
         per_cu = std::max(per_cu, 1);
-        const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(static_cast<int64_t>(per_cu) * info.sm_count,
-                                                                      total));
-        std::vector<int64_t> p_off(nq);
-        std::vector<int32_t> p_len(nq);
-        int64_t pairs = 0;
-        for (size_t qi = 0; qi < nq; ++qi) {
-            int64_t count = 0;
-            if (q_gran[qi + 1] > q_gran[qi])
-                count = vk::first_block_of(q_gran[qi + 1] - 1, grid, total) -
-                        vk::first_block_of(q_gran[qi], grid, total) + 1;
-            p_off[qi] = pairs;
-            p_len[qi] = static_cast<int32_t>(count * W * K);
-            pairs += count * W * K;
-        }
+        const int64_t grid = static_cast<int64_t>(per_cu) * info.sm_count;
+        part.ensure(static_cast<size_t>(grid + static_cast<int64_t>(nq)) * W * K);  // lists of block b, query q at b + q
 
         last = vk_launch_shape{};
         last.threads = kern.threads;
@@ -905,60 +877,31 @@ struct vk_ivf {
         last.queries_per_block = 1;
         last.vectors_per_step = 4;
         last.blocks_per_sm = per_cu;
-        last.waves = static_cast<double>(grid) / (static_cast<double>(per_cu) * info.sm_count);
+        last.waves = 1.0;
 
-        part.ensure(static_cast<size_t>(std::max<int64_t>(pairs, 1)));
-        part_offset.ensure(nq);
-        seg_len.ensure(nq);
-        query_gran.ensure(nq + 1);
-        clock.time(&t->transfer_ms, [&] {
-            if (n_slabs > 0) {
-                slab_list.ensure(s_list.size());
-                slab_queries.ensure(s_query.size());
-                slab_gran.ensure(s_gran.size());
-                VK_HIP(hipMemcpyAsync(slab_list.get(), s_list.data(), s_list.size() * sizeof(int32_t),
-                                      hipMemcpyHostToDevice, stream));
-                VK_HIP(hipMemcpyAsync(slab_queries.get(), s_query.data(), s_query.size() * sizeof(int32_t),
-                                      hipMemcpyHostToDevice, stream));
-                VK_HIP(hipMemcpyAsync(slab_gran.get(), s_gran.data(), s_gran.size() * sizeof(int64_t),
-                                      hipMemcpyHostToDevice, stream));
-            }
-            VK_HIP(hipMemcpyAsync(query_gran.get(), q_gran.data(), q_gran.size() * sizeof(int64_t),
-                                  hipMemcpyHostToDevice, stream));
-            VK_HIP(hipMemcpyAsync(part_offset.get(), p_off.data(), p_off.size() * sizeof(int64_t),
-                                  hipMemcpyHostToDevice, stream));
-            VK_HIP(hipMemcpyAsync(seg_len.get(), p_len.data(), p_len.size() * sizeof(int32_t), hipMemcpyHostToDevice,
-                                  stream));
-        });
-
-        // 4. the scan over the probed lists, then the per-query merge
-        if (total > 0) {
-            vk::WaveScanArgs a{};
-            a.queries = d_q;
-            a.centroids = centroids.get();
-            a.codes = codes_v.get();
-            a.n = static_cast<int64_t>(n);
-            a.d = static_cast<int>(d);
-            a.m = static_cast<int>(m);
-            a.nq = static_cast<int>(nq);
-            a.K = K;
-            a.k = static_cast<int>(kk);
-            a.total = total;
-            a.lists_per_block = W;
-            a.part = part.get();
-            a.n_slabs = n_slabs;
-            a.slab_gran = slab_gran.get();
-            a.slab_list = slab_list.get();
-            a.slab_queries = slab_queries.get();
-            a.query_gran = query_gran.get();
-            a.list_tile = list_tile.get();
-            a.ids = ids.get();
-            a.part_offset = part_offset.get();
-            a.lut = lut.get();
-            clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(grid), smem, stream)); });
-        }
-        vk::IvfMergeArgs ma{part.get(), part_offset.get(), seg_len.get(), static_cast<int64_t>(nq), K,
-                            static_cast<int>(kk), d_o};
+        vk::WaveScanArgs a{};
+        a.queries = d_q;
+        a.centroids = centroids.get();
+        a.codes = codes_v.get();
+        a.n = static_cast<int64_t>(n);
+        a.d = static_cast<int>(d);
+        a.m = static_cast<int>(m);
+        a.nq = static_cast<int>(nq);
+        a.K = K;
+        a.k = static_cast<int>(kk);
+        a.lists_per_block = W;
+        a.part = part.get();
+        a.n_slabs = static_cast<int64_t>(slabs);
+        a.slab_gran = slab_gran.get();
+        a.slab_list = slab_list.get();
+        a.slab_queries = slab_queries.get();
+        a.query_gran = query_gran.get();
+        a.list_tile = list_tile.get();
+        a.ids = ids.get();
+        a.lut = lut.get();
+        clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(grid), smem, stream)); });
+        vk::IvfMergeArgs ma{part.get(), query_gran.get(), grid, W, static_cast<int64_t>(nq), K, static_cast<int>(kk),
+                            d_o};
         clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_ivf_merge(ma, stream)); });
     }
 };

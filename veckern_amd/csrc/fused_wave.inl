@@ -377,11 +377,11 @@ __device__ __forceinline__ int64_t slab_of(const int64_t* slab_gran, int64_t sla
 
 // IVF (one query per slab, QS = 1): the scan runs over inverted lists. Slab s is list a.slab_list[s] probed by
 // query a.slab_queries[s]; slabs are in query-major order, so a query's probed lists form one run of consecutive
-// slabs, granules [a.query_gran[q], a.query_gran[q + 1]) of the balanced partition. Slab s covers granules
-// [a.slab_gran[s], a.slab_gran[s + 1]), its list's padded tiles start at a.list_tile[list] in the
-// word-interleaved codes, and the vector ids come from a.ids (-1 on padding). A block gathers a query's tables and
-// starts its lists once per run and writes them once, at the end of the run (or of its range); a separate merge
-// kernel combines the partial lists of each query.
+// slabs, granules [a.query_gran[q], a.query_gran[q + 1]) of the balanced partition (a.query_gran[nq] = total).
+// Slab s covers granules [a.slab_gran[s], a.slab_gran[s + 1]) (possibly none), its list's padded tiles start at
+// a.list_tile[list] in the word-interleaved codes, and the vector ids come from a.ids (-1 on padding). A block
+// gathers a query's tables and starts its lists once per run and writes them once, at the end of the run (or of
+// its range); a separate merge kernel combines the partial lists of each query.
 template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF>
 __global__ void __launch_bounds__(T)
     __attribute__((amdgpu_waves_per_eu(wave_kernel_waves_per_simd<QG, NG, M, T, F16>())))
@@ -414,8 +414,13 @@ __global__ void __launch_bounds__(T)
     // The wave index is the same in every lane; reading it through a scalar register lets the compiler keep the
     // granule, tile and id arithmetic of the scan loop on the scalar unit.
     const int tid = threadIdx.x, lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
-    const int64_t grid = gridDim.x, b = blockIdx.x;
-    const int64_t start = b * a.total / grid, end = (b + 1) * a.total / grid;
+    // Inverted lists are planned on the device: the total is read here, and with fewer granules than blocks only
+    // the first `total` blocks take part, so that every block of the partition owns at least one granule (the
+    // merge kernel expects lists from every block between a query's first and last).
+    const int64_t total = IVF ? a.query_gran[a.nq] : a.total;
+    const int64_t grid = IVF ? min<int64_t>(gridDim.x, total) : gridDim.x, b = blockIdx.x;
+    if (IVF && b >= grid) return;  // block-uniform, before any barrier
+    const int64_t start = b * total / grid, end = (b + 1) * total / grid;
     const _Float16 one = opaque_half_one();
 
     // Inverted lists: the first slab of the block's range by binary search; every later one is the next slab
@@ -433,7 +438,10 @@ __global__ void __launch_bounds__(T)
         // The slab holding `item` and its granules [slab_first, slab_next) in the balanced partition.
         int64_t slab, slab_first, slab_next;
         if constexpr (IVF) {
-            slab = next_slab++;
+            // Probes of no list or of an empty list are empty slabs: skipped (a non-empty slab holds `item`).
+            slab = next_slab;
+            while (a.slab_gran[slab + 1] == a.slab_gran[slab]) ++slab;
+            next_slab = slab + 1;
             slab_first = a.slab_gran[slab];
             slab_next = a.slab_gran[slab + 1];
         } else {
@@ -605,22 +613,21 @@ __global__ void __launch_bounds__(T)
         }
 
         // Inverted lists: when the query's run of slabs ends (or the block's range does), every wave writes its
-        // list for the query at part[part_offset[query] + (slot * W + wave) * K], slot = this block's index among
-        // the blocks that cover the run; the merge kernel combines them.
+        // list for the query at part[((b + query) * W + wave) * K]. Along the granule order both the block and the
+        // query only grow and one of them grows at every new (block, query) pair, so b + query is unique per pair
+        // and a query's lists (from consecutive blocks) are contiguous for the merge kernel.
         if constexpr (IVF) {
             item = slab_next;
-            if (item >= end || a.slab_queries[next_slab] != run_query) {  // next_slab < n_slabs when item < end
-                const int64_t lo = first_block_of(a.query_gran[run_query], grid, a.total);
-                lists[0].store(a.part + a.part_offset[run_query] + ((b - lo) * W + wave) * a.K, a.K);
-            }
+            if (item >= end || item >= a.query_gran[run_query + 1])
+                lists[0].store(a.part + ((b + run_query) * W + wave) * a.K, a.K);
             continue;
         }
 
         // Partial lists of this (block, slab): part[slab][q][slot][list][K], the lists of one query contiguous.
         // With few blocks per slab every wave writes its own lists; with many, the block first merges its W lists
         // per query in LDS (the tables are dead by then), so the final merge reads W times fewer pairs.
-        const int64_t lo = first_block_of(slab_first, grid, a.total);
-        const int count = static_cast<int>(first_block_of(slab_next - 1, grid, a.total) - lo + 1);
+        const int64_t lo = first_block_of(slab_first, grid, total);
+        const int count = static_cast<int>(first_block_of(slab_next - 1, grid, total) - lo + 1);
         const int slot = static_cast<int>(b - lo);
         const int lpb = a.lists_per_block;
         const int slots = a.max_slots;  // every slab reserves max_slots blocks

@@ -1,7 +1,8 @@
 // Inverted-file (IVF) search, the reference's "coarse partitioning" next step (README.md:219): per query, the
 // nprobe nearest coarse centroids (exact distances, the re-rank kernel with every list as a candidate), then the
 // fused wave-list scan over only those lists' PQ codes (fused_wave.inl with IVF = true: slabs = (query, probed
-// list) in query-major order), then this file's merge of each query's partial lists.
+// list) in query-major order), then this file's merge of each query's partial lists. The slab plan is built on
+// the device from the probes (this file's plan kernels), so a search makes no host round trip before its results.
 #include "kernels.hpp"
 
 namespace vk {
@@ -23,9 +24,85 @@ WaveScanKernel ivf_kernel(int m, int segments) {
 namespace {
 
 constexpr int kMergeThreads = 256;
+constexpr int kPlanThreads = 256;
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ int64_t wave_inclusive_sum(int64_t v) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int64_t up = __shfl_up(v, o);
+        if (lane >= o) v += up;
+    }
+    return v;
+}
+
+// Plan, step 1 (one wave per query): slab q * nprobe + p is query q's p-th probed list; its granule count is the
+// list's padded tiles / 4 (0 for a probe of no list). slab_gran receives each slab's start within its query's run
+// and query_gran[q] the run's length.
+__global__ void __launch_bounds__(kPlanThreads) ivf_plan_runs_kernel(IvfPlanArgs a) {
+    const int lane = __lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / WAVE);
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * (kPlanThreads / WAVE) + wave;
+    if (q >= a.nq) return;  // wave-uniform
+    int64_t run = 0;
+    for (int base = 0; base < a.nprobe; base += WAVE) {
+        const int p = base + lane;
+        int32_t list = 0;
+        int64_t gran = 0;
+        if (p < a.nprobe) {
+            const int32_t l = a.probes[q * a.nprobe + p].i;
+            if (l >= 0) {  // a query whose coarse distances are all NaN probes nothing
+                list = l;
+                gran = (a.list_tile[l + 1] - a.list_tile[l]) / 4;
+            }
+        }
+        const int64_t incl = wave_inclusive_sum(gran);
+        if (p < a.nprobe) {
+            const int64_t s = q * a.nprobe + p;
+            a.slab_list[s] = list;
+            a.slab_queries[s] = static_cast<int32_t>(q);
+            a.slab_gran[s] = run + incl - gran;
+        }
+        run += __shfl(incl, WAVE - 1);
+    }
+    if (lane == 0) a.query_gran[q] = run;
+}
+
+// Plan, step 2 (one block): query_gran[0..nq) from run lengths to their exclusive prefix, query_gran[nq] = total.
+__global__ void __launch_bounds__(kScanThreads) ivf_plan_scan_kernel(IvfPlanArgs a) {
+    __shared__ int64_t wave_sums[kScanThreads / WAVE];
+    const int tid = threadIdx.x, lane = __lane_id(), wave = tid / WAVE;
+    const int64_t per = (a.nq + kScanThreads - 1) / kScanThreads;
+    const int64_t lo = min<int64_t>(a.nq, tid * per), hi = min<int64_t>(a.nq, lo + per);
+    int64_t sum = 0;
+    for (int64_t i = lo; i < hi; ++i) sum += a.query_gran[i];
+    const int64_t incl = wave_inclusive_sum(sum);
+    if (lane == WAVE - 1) wave_sums[wave] = incl;
+    __syncthreads();
+    int64_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_sums[w];
+    int64_t run = before + incl - sum;
+    for (int64_t i = lo; i < hi; ++i) {
+        const int64_t len = a.query_gran[i];
+        a.query_gran[i] = run;
+        run += len;
+    }
+    if (tid == kScanThreads - 1) a.query_gran[a.nq] = run;
+}
+
+// Plan, step 3 (one thread per slab): slab starts from run-relative to absolute; slab_gran[n_slabs] = total.
+__global__ void __launch_bounds__(kPlanThreads) ivf_plan_offsets_kernel(IvfPlanArgs a) {
+    const int64_t s = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x;
+    const int64_t slabs = a.nq * a.nprobe;
+    if (s < slabs) a.slab_gran[s] += a.query_gran[s / a.nprobe];
+    if (s == slabs) a.slab_gran[s] = a.query_gran[a.nq];
+}
 
 // One wave per query streams the pairs of its partial lists through a wave list (four 64-pair chunks in flight
-// per round) and writes the k best, empty slots as {+inf, -1}.
+// per round) and writes the k best, empty slots as {+inf, -1}. The lists of query q are those of the blocks
+// b_lo .. b_hi that cover its run, at (b + q) * W * K (the scan's layout), so one contiguous range; the scan used
+// min(grid, total) blocks, each owning at least one granule, so every block of that range wrote its lists.
 template <int S>
 __global__ void __launch_bounds__(kMergeThreads) ivf_merge_kernel(IvfMergeArgs a) {
     const int lane = __lane_id();
@@ -34,14 +111,21 @@ __global__ void __launch_bounds__(kMergeThreads) ivf_merge_kernel(IvfMergeArgs a
     if (q >= a.nq) return;  // wave-uniform
     WaveList<S> wl;
     wl.init();
-    const Pair* first = a.part + a.seg_off[q];
-    const int len = a.seg_len[q];
+    const int64_t r_first = a.query_gran[q], r_next = a.query_gran[q + 1], total = a.query_gran[a.nq];
+    const int64_t grid = min(a.grid, total);  // the blocks that took part in the scan
+    int64_t len = 0;
+    const Pair* first = a.part;
+    if (r_next > r_first) {  // an empty run (no probed vectors) has no lists: all slots stay empty
+        const int64_t b_lo = first_block_of(r_first, grid, total), b_hi = first_block_of(r_next - 1, grid, total);
+        first = a.part + (b_lo + q) * a.lists_per_block * a.K;
+        len = (b_hi - b_lo + 1) * a.lists_per_block * a.K;
+    }
     constexpr int B = 4;
-    for (int base = 0; base < len; base += B * WAVE) {
+    for (int64_t base = 0; base < len; base += B * WAVE) {
         Pair e[B];
 #pragma unroll
         for (int u = 0; u < B; ++u) {
-            const int j = base + u * WAVE + lane;
+            const int64_t j = base + u * WAVE + lane;
             e[u] = j < len ? first[j] : Pair{INFINITY, kEmptyId};
         }
 #pragma unroll
@@ -56,6 +140,18 @@ __global__ void __launch_bounds__(kMergeThreads) ivf_merge_kernel(IvfMergeArgs a
 }
 
 }  // namespace
+
+hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t stream) {
+    if (a.nq <= 0 || a.nprobe <= 0) return hipErrorInvalidValue;
+    const int waves = kPlanThreads / WAVE;
+    hipLaunchKernelGGL(ivf_plan_runs_kernel, dim3(static_cast<unsigned>((a.nq + waves - 1) / waves)),
+                       dim3(kPlanThreads), 0, stream, a);
+    hipLaunchKernelGGL(ivf_plan_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, a);
+    const int64_t slabs = a.nq * a.nprobe + 1;
+    hipLaunchKernelGGL(ivf_plan_offsets_kernel, dim3(static_cast<unsigned>((slabs + kPlanThreads - 1) / kPlanThreads)),
+                       dim3(kPlanThreads), 0, stream, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_ivf_merge(const IvfMergeArgs& a, hipStream_t stream) {
     const int waves_per_block = kMergeThreads / WAVE;

@@ -40,7 +40,8 @@ struct WaveScanArgs {
     Pair* part;              // [slabs][qg * ng][max_slots][lists_per_block][K]
     unsigned* counters;      // [slabs], zero between searches: blocks of a slab that have finished
     Pair* out;               // [nq][k]; empty slots become {+inf, -1}
-    // Inverted lists (IVF instances only, one query per slab); `n_gran` and `max_slots` are then unused.
+    // Inverted lists (IVF instances only, one query per slab, the plan of launch_ivf_plan); `n_gran`, `total` and
+    // `max_slots` are then unused (the total is query_gran[nq]).
     int64_t n_slabs;
     const int64_t* slab_gran;      // [n_slabs + 1] granule prefix of the slabs
     const int32_t* slab_list;      // [n_slabs] list scanned by each slab
@@ -48,7 +49,6 @@ struct WaveScanArgs {
     const int64_t* query_gran;     // [nq + 1] granule prefix of the queries' runs of slabs
     const int64_t* list_tile;      // [lists + 1] first tile of each list in `codes` / `ids`
     const int32_t* ids;            // [tiles * 64] vector id of each padded position, -1 for padding
-    const int64_t* part_offset;    // [nq] first pair of each query's partial lists in `part`
     const float* lut;              // [nq][m][256] tables computed once per search (a query meets many lists)
 };
 
@@ -64,12 +64,29 @@ WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, b
 // The inverted-list scan (ivf_m*.hip): fp32 tables, one query per slab, four tiles per wave step.
 WaveScanKernel ivf_kernel(int m, int segments);
 
-// ---- IVF final merge (ivf.hip): query q's partial lists are the pairs part[seg_off[q] .. + seg_len[q]); its k
-// results go to out[q * k].
+// ---- IVF plan (ivf.hip): from the probes (nq x nprobe, id -1 = no list), slab q * nprobe + p = query q's p-th
+// probed list: slab_list / slab_queries [nq * nprobe], slab_gran [nq * nprobe + 1] (granule starts; a probe of no
+// list or of an empty list is an empty slab), query_gran [nq + 1] (the granule start of each query's run; the last
+// entry is the total).
+struct IvfPlanArgs {
+    const Pair* probes;
+    int nprobe;
+    int64_t nq;
+    const int64_t* list_tile;
+    int32_t* slab_list;
+    int32_t* slab_queries;
+    int64_t* slab_gran;
+    int64_t* query_gran;
+};
+hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t stream);
+
+// ---- IVF final merge (ivf.hip): block b of the scan (grid blocks, lists_per_block lists of K pairs each) writes
+// its lists for query q at part[(b + q) * lists_per_block * K]; the k results of q go to out[q * k].
 struct IvfMergeArgs {
     const Pair* part;
-    const int64_t* seg_off;
-    const int32_t* seg_len;
+    const int64_t* query_gran;
+    int64_t grid;
+    int lists_per_block;
     int64_t nq;
     int K;
     int k;
