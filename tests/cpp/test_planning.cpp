@@ -62,6 +62,10 @@ CASE("blocks_x_fill: ~8 blocks per CU over the grid, >= 16 vectors per thread, o
 }
 
 CASE("balanced_partition covers every item exactly once and bounds the slots per slab") {
+    // one slab on 256 CUs with two resident blocks each: one block per CU, not two
+    EXPECT(balanced_partition(10'000'000, 1, 1, 4, 512, 0, 256).grid == 256);
+    EXPECT(balanced_partition(10'000'000, 2, 1, 4, 512, 0, 256).grid == 512);
+    EXPECT(balanced_partition(10'000'000, 1, 1, 4, 512, 0).grid == 512);
     std::mt19937_64 rng(7);
     for (int trial = 0; trial < 300; ++trial) {
         const int64_t n = 1 + static_cast<int64_t>(rng() % 200'000);
@@ -70,11 +74,13 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
         const int ilp = 1 << (rng() % 3);
         const int64_t slots = 1 + static_cast<int64_t>(rng() % 1100);
         const int bpq = (trial % 3 == 0) ? static_cast<int>(1 + rng() % 40) : 0;
-        const Partition p = balanced_partition(n, nq, q, ilp, slots, bpq);
+        const int64_t cus = (trial % 2 == 0) ? 1 + static_cast<int64_t>(rng() % 300) : 0;
+        const Partition p = balanced_partition(n, nq, q, ilp, slots, bpq, cus);
         EXPECT(p.slabs == static_cast<int64_t>((nq + q - 1) / q));
         EXPECT(p.n_gran == ((n + 63) / 64 + ilp - 1) / ilp);
         EXPECT(p.total == p.slabs * p.n_gran && p.grid >= 1 && p.grid <= p.total);
         if (bpq == 0) EXPECT(p.grid <= slots);
+        if (bpq == 0 && cus > 0) EXPECT(p.grid <= p.slabs * cus);  // a slab never gets more blocks than CUs
         // block ranges tile [0, total) in order, and every block is non-empty
         int64_t prev_end = 0;
         for (int64_t b = 0; b < p.grid; ++b) {

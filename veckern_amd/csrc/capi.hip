@@ -257,7 +257,8 @@ struct vk_searcher {
         per_cu = std::max(per_cu, 1);
 
         const vk::plan::Partition part_plan = vk::plan::balanced_partition(
-            static_cast<int64_t>(n), b, q, ilp, static_cast<int64_t>(per_cu) * info.sm_count, tuning.blocks_per_query);
+            static_cast<int64_t>(n), b, q, ilp, static_cast<int64_t>(per_cu) * info.sm_count, tuning.blocks_per_query,
+            info.sm_count);
         // Up to 8 blocks per slab every wave leaves its own partial lists; beyond that the block merges its wave
         // lists first, which keeps the final merge of a slab to at most max(64, blocks per slab) lists per query.
         const int lists_per_block = part_plan.max_slots > 8 ? 1 : kern.threads / vk::WAVE;

@@ -302,10 +302,11 @@ __device__ __forceinline__ Pair final_pair(float d, int32_t id, int shift) {
 }
 
 // Streams pairs [begin, all) of consecutive partial lists through a wave list: four 64-pair chunks per round (four
-// loads in flight), rounds `step` pairs apart so that several waves can split one range.
+// loads in flight), rounds `step` pairs apart so that several waves can split one range. The lists are merged with
+// bulk admission (device.hpp): a chunk of sorted partial lists admits many pairs at once while the list fills.
 template <int S>
-__device__ __forceinline__ void stream_pairs(WaveList<S>& wl, const Pair* first, int begin, int step, int all, int K,
-                                             int lane) {
+__device__ __forceinline__ void stream_pairs(WaveList<S, true>& wl, const Pair* first, int begin, int step, int all,
+                                             int K, int lane) {
     constexpr int B = 4;
     for (int base = begin; base < all; base += step) {
         Pair p[B];
@@ -324,7 +325,7 @@ __device__ __forceinline__ void stream_pairs(WaveList<S>& wl, const Pair* first,
 template <int S>
 __device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, int K, int k, Pair* out, int shift,
                                                  int lane) {
-    WaveList<S> wl;
+    WaveList<S, true> wl;
     wl.init();
     stream_pairs(wl, first, 0, 4 * WAVE, lists * K, K, lane);
 #pragma unroll
@@ -341,7 +342,7 @@ __device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, i
 template <int S, int W>
 __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K, int k, Pair* out, int shift,
                                             Pair* buf, int tid, int wave, int lane) {
-    WaveList<S> wl;
+    WaveList<S, true> wl;
     wl.init();
     stream_pairs(wl, first, wave * 4 * WAVE, W * 4 * WAVE, lists * K, K, lane);
     wl.store(buf + wave * K, K);
