@@ -173,8 +173,8 @@ int vk_rerank_device(vk_reranker* r, const float* d_queries, size_t nq, const vk
  * whose coarse centroids are nearest (exact squared L2, ties to the lower list id) and returns the k best vectors
  * of those lists by (ADC distance, id), padded {+inf, -1}: the exhaustive search (vk_search) restricted to the
  * probed lists, with bit-identical distances. m % 16 == 0; nprobe in [1, min(128, nlist)]; k in [1, min(128, n)].
- * Timings: lut_ms = coarse probe kernel, scan_ms = list scan, select_ms = merge, transfer_ms = host copies
- * (queries, per-search list grouping built on the host, results). */
+ * Timings: lut_ms = coarse probe, table and plan kernels, scan_ms = list scan, select_ms = merge, transfer_ms =
+ * host copies of queries and results (none for vk_ivf_search_device). */
 int vk_ivf_create(const float* coarse, size_t nlist, const float* centroids, size_t d, size_t m, const uint8_t* codes,
                   const int32_t* list_ids, size_t n, vk_ivf** out);
 void vk_ivf_destroy(vk_ivf* index);
@@ -187,6 +187,10 @@ int vk_ivf_set_tuning(vk_ivf* index, const vk_tuning* t);
 int vk_ivf_last_launch(const vk_ivf* index, vk_launch_shape* out);
 int vk_ivf_search(vk_ivf* index, const float* queries, size_t nq, size_t nprobe, size_t k, vk_neighbor* out,
                   vk_timings* timings);
+/* Device-resident IVF search: d_queries (nq x d floats) and d_out (nq x k vk_neighbor) are device pointers on the
+ * index's device; no transfer is made or timed. Like vk_search_device, no counterpart in the reference. */
+int vk_ivf_search_device(vk_ivf* index, const float* d_queries, size_t nq, size_t nprobe, size_t k,
+                         vk_neighbor* d_out, vk_timings* timings);
 
 /* PQ encoding on the GPU: ProductQuantizer::encode (pq.hpp:36, pq.cpp:70-75). codes[i * m + s] is the first
  * c in 0..255 with the smallest l2sq(x_i's sub-vector s, centroids[s][c]) (nearest_centroid, pq.cpp:11-22: a

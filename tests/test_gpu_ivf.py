@@ -124,3 +124,18 @@ def test_ivf_assign_is_the_nearest_coarse_centroid():
     cand["id"] = np.arange(300)
     exp = orc.rerank_exact(coarse, x, cand, 1)["id"][:, 0]
     assert (got == exp).all() and (got[:50] == 20).all()
+
+
+def test_ivf_device_resident_search_matches_host_buffers(index_case):
+    (coarse, cent, codes, list_ids, queries), ix = index_case
+    nq, k = queries.shape[0], 10
+    dq = vk.DeviceArray.from_host(np.ascontiguousarray(queries, dtype=np.float32))
+    dout = vk.DeviceArray(nq * k * vk.NEIGHBOR_DTYPE.itemsize)
+    try:
+        t = ix.search_device(dq.address, nq, 16, k, dout.address)
+        got = dout.download(np.empty((nq, k), dtype=vk.NEIGHBOR_DTYPE))
+    finally:
+        dq.free()
+        dout.free()
+    assert t.transfer_ms == 0 and t.scan_ms > 0
+    assert_same(got["dist"], got["id"], orc.ivf_search(coarse, cent, 64, codes, list_ids, queries, 16, k), "device")

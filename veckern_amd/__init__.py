@@ -119,6 +119,8 @@ _SIGNATURES = {
     "vk_ivf_last_launch": (ctypes.c_int, [_P, ctypes.POINTER(_LaunchShape)]),
     "vk_ivf_search": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _P,
                                      ctypes.POINTER(_Timings)]),
+    "vk_ivf_search_device": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _P,
+                                            ctypes.POINTER(_Timings)]),
     "vk_pq_encode": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
     "vk_pq_encode_device": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
     "vk_pq_assign": (ctypes.c_int, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
@@ -426,6 +428,13 @@ class IVFIndex:
         _check(library().vk_ivf_search(self._h, q.ctypes.data, q.shape[0], nprobe, k, out.ctypes.data,
                                        ctypes.byref(t)))
         return out["dist"].copy(), out["id"].copy(), _timings(t)
+
+    def search_device(self, d_queries: int, nq: int, nprobe: int, k: int, d_out: int) -> Timings:
+        """Device-resident search: d_queries / d_out are device addresses (nq x d float32, nq x k pairs)."""
+        t = _Timings()
+        _check(library().vk_ivf_search_device(self._h, ctypes.c_void_p(d_queries), nq, nprobe, k,
+                                              ctypes.c_void_p(d_out), ctypes.byref(t)))
+        return _timings(t)
 
 
 class Reranker:

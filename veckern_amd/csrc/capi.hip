@@ -1050,6 +1050,27 @@ VK_EXPORT int vk_ivf_search(vk_ivf* v, const float* queries, size_t nq, size_t n
     });
 }
 
+VK_EXPORT int vk_ivf_search_device(vk_ivf* v, const float* d_queries, size_t nq, size_t nprobe, size_t k,
+                                   vk_neighbor* d_out, vk_timings* timings) {
+    return guarded([&] {
+        require(v != nullptr, "index is null");
+        v->check(nprobe, k);
+        vk_timings t{};
+        if (nq > 0) {
+            require(d_queries != nullptr && d_out != nullptr, "queries and out must not be null");
+            VK_HIP(hipSetDevice(v->device));
+            StageClock clock(v->stream);
+            const size_t batch = 16384;  // queries per batch, as in vk_ivf_search
+            for (size_t q0 = 0; q0 < nq; q0 += batch) {
+                const size_t b = std::min(batch, nq - q0);
+                v->search(d_queries + q0 * v->d, b, nprobe, k, reinterpret_cast<Pair*>(d_out) + q0 * k, &t, clock);
+                clock.settle();
+            }
+        }
+        if (timings) *timings = t;
+    });
+}
+
 VK_EXPORT int vk_reranker_create(const float* base, size_t n, size_t d, vk_reranker** out) {
     return guarded([&] {
         require(out != nullptr, "out is null");
