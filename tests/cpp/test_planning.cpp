@@ -66,6 +66,11 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
     EXPECT(balanced_partition(10'000'000, 1, 1, 4, 512, 0, 256).grid == 256);
     EXPECT(balanced_partition(10'000'000, 2, 1, 4, 512, 0, 256).grid == 512);
     EXPECT(balanced_partition(10'000'000, 1, 1, 4, 512, 0).grid == 512);
+    // slabs no more than the slots: floor(slots / slabs) whole blocks per slab (1M x nq=1000 at Q = 4: 2 each)
+    const Partition b = balanced_partition(1'000'000, 1000, 4, 4, 512, 0, 256);
+    EXPECT(b.grid == 500 && b.max_slots == 2);
+    EXPECT(balanced_partition(1'000'000, 1000, 4, 4, 256, 0, 256).grid == 250);  // one block per slab
+    EXPECT(balanced_partition(1'000'000, 1000, 2, 4, 256, 0, 256).grid == 256);  // 500 slabs > 256 slots
     std::mt19937_64 rng(7);
     for (int trial = 0; trial < 300; ++trial) {
         const int64_t n = 1 + static_cast<int64_t>(rng() % 200'000);
@@ -81,6 +86,8 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
         EXPECT(p.total == p.slabs * p.n_gran && p.grid >= 1 && p.grid <= p.total);
         if (bpq == 0) EXPECT(p.grid <= slots);
         if (bpq == 0 && cus > 0) EXPECT(p.grid <= p.slabs * cus);  // a slab never gets more blocks than CUs
+        const bool aligned = bpq > 0 || p.slabs <= slots;  // whole blocks per slab: no block crosses a boundary
+        if (aligned) EXPECT(p.grid % p.slabs == 0);
         // block ranges tile [0, total) in order, and every block is non-empty
         int64_t prev_end = 0;
         for (int64_t b = 0; b < p.grid; ++b) {
@@ -95,8 +102,7 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
             const int64_t hi = first_block((slab + 1) * p.n_gran - 1, p.grid, p.total);
             EXPECT(lo * p.total / p.grid <= slab * p.n_gran && slab * p.n_gran < (lo + 1) * p.total / p.grid);
             EXPECT(hi - lo + 1 <= p.max_slots);
-            if (bpq > 0 && p.grid == p.slabs * std::min<int64_t>(bpq, p.n_gran))
-                EXPECT(hi - lo + 1 == std::min<int64_t>(bpq, p.n_gran));
+            if (aligned) EXPECT(hi - lo + 1 == p.grid / p.slabs && lo == slab * (p.grid / p.slabs));
         }
     }
 }

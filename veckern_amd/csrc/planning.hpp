@@ -40,10 +40,13 @@ inline int cap_q_by_batch(int q, size_t nq) {
 inline int64_t first_block(int64_t item, int64_t grid, int64_t total) { return ((item + 1) * grid - 1) / total; }
 
 // Balanced partition of the wave-list scan: slabs of q queries, each cut into granules of 64*ilp vectors;
-// the slabs*n_gran items are split evenly over `grid` blocks. grid = resident blocks (slots) unless
-// blocks_per_query asks for a fixed number of blocks per slab. With `cus` > 0 a slab gets at most that many blocks
-// (one per CU): the slab's final merge grows with its blocks, and once every CU holds a block of the slab a second
-// one no longer speeds the scan (measured at nq = 1: 10M vectors, 73 -> 67 us; 1M at k = 100, 131 -> 104 us).
+// the slabs*n_gran items are split evenly over `grid` blocks. blocks_per_query > 0 fixes the blocks per slab.
+// Otherwise, when the slabs are no more than the resident blocks (`slots`), each slab gets floor(slots / slabs)
+// blocks, at most `cus` (> 0) of them, so that no block crosses a slab boundary; with more slabs than slots,
+// grid = slots and blocks span slab boundaries. Measured on MI355X: with a block per resident slot and ranges
+// crossing slabs, the two blocks sharing a CU finish ~0.4 ms apart at 1M x nq=1000 (the older block's waves get
+// issue priority) and the search takes 1.43 ms; slab-aligned blocks take 1.35 ms (fp16 tables at Q = 8: 1.07 ->
+// 0.90 ms). A slab's blocks beyond one per CU only lengthen its final merge (nq = 1 at 10M: 73 -> 67 us).
 struct Partition {
     int64_t slabs = 0, n_gran = 0, total = 0, grid = 0;
     int max_slots = 0;  // most blocks touching one slab = partial lists per query
@@ -56,11 +59,16 @@ inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_
     const int64_t tiles = (n + 63) / 64;
     p.n_gran = (tiles + ilp - 1) / ilp;
     p.total = p.slabs * p.n_gran;
-    if (blocks_per_query > 0)
-        p.grid = p.slabs * std::min<int64_t>(blocks_per_query, p.n_gran);
+    slots = std::max<int64_t>(slots, 1);
+    int64_t per_slab = blocks_per_query;
+    if (per_slab <= 0 && p.slabs <= slots) {
+        per_slab = slots / p.slabs;
+        if (cus > 0) per_slab = std::min(per_slab, cus);
+    }
+    if (per_slab > 0)
+        p.grid = p.slabs * std::min<int64_t>(per_slab, p.n_gran);
     else
-        p.grid = std::min<int64_t>(std::max<int64_t>(slots, 1), p.total);
-    if (blocks_per_query <= 0 && cus > 0) p.grid = std::min(p.grid, p.slabs * cus);
+        p.grid = std::min<int64_t>(slots, p.total);
     // Keep grid * total (the kernel's range arithmetic) and the grid size itself in range.
     const int64_t limit = std::min<int64_t>(int64_t{1} << 31 >> 1, (int64_t{1} << 62) / std::max<int64_t>(p.total, 1));
     p.grid = std::max<int64_t>(1, std::min(p.grid, limit));
