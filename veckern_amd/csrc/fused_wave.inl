@@ -399,6 +399,10 @@ __global__ void __launch_bounds__(T)
     __shared__ uint4 lds_static[kStaticVec];
     extern __shared__ uint4 lds_dynamic[];
     __shared__ bool last_block;
+    // Exhaustive search: granules of the block's range past the first W, handed out one at a time to whichever wave
+    // asks next. With static assignment the waves a SIMD favours finish their share first and leave one wave per
+    // SIMD to finish the block, too few to keep the LDS pipe busy.
+    __shared__ unsigned next_gran;
     __shared__ unsigned qmax[QS];  // fp16 tables: per-query maximum entry of the current slab (raw bits)
     // Long lists (K > 64) only: per (query, wave), the distance of the wave list's entry ceil(K/W) - 1 for the
     // current slab (raw bits of a distance >= 0, so unsigned order is float order; +inf until the list holds that
@@ -491,6 +495,7 @@ __global__ void __launch_bounds__(T)
             else build_tables<QG, NG, M, W, F16>(a, qrow, tables, table_bytes, qmax, wave, lane);
             if constexpr (kShareBound)
                 for (int t = tid; t < QS * W; t += T) (&rank_bound[0][0])[t] = 0x7f800000u;  // +inf
+            if (!IVF && tid == 0) next_gran = W;
             __syncthreads();
 
             // A padded query slot (past nq in the last slab) gets the threshold -inf: no distance passes it, so
@@ -504,7 +509,11 @@ __global__ void __launch_bounds__(T)
         }
         const uint32_t n32 = static_cast<uint32_t>(a.n);  // n < 2^31: ids and tile bounds fit in 32 bits
 
-        for (int64_t g = g_lo + wave; g < g_hi; g += W) {
+        for (int64_t g = g_lo + wave; g < g_hi;) {
+            // The next granule for this wave, asked for now and used after this one (inverted lists: every W-th).
+            unsigned grab = 0;
+            if constexpr (!IVF)
+                if (lane == 0) grab = atomicAdd(&next_gran, 1u);
             // The block's bound per query (a stale slot only loosens it: published values only fall).
             if constexpr (kShareBound) {
 #pragma unroll
@@ -611,6 +620,8 @@ __global__ void __launch_bounds__(T)
                     }
                 }
             }
+            if constexpr (IVF) g += W;
+            else g = g_lo + static_cast<int64_t>(__builtin_amdgcn_readfirstlane(grab));
         }
 
         // Inverted lists: when the query's run of slabs ends (or the block's range does), every wave writes its
