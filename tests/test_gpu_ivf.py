@@ -139,3 +139,18 @@ def test_ivf_device_resident_search_matches_host_buffers(index_case):
         dout.free()
     assert t.transfer_ms == 0 and t.scan_ms > 0
     assert_same(got["dist"], got["id"], orc.ivf_search(coarse, cent, 64, codes, list_ids, queries, 16, k), "device")
+
+
+def test_ivf_probe_ties_go_to_the_lower_list():
+    # duplicated coarse centroids and queries sitting exactly on them: equal probe distances, the lower list id
+    # must be probed first (the reference's (dist, id) order); also d not a multiple of the probe's 32-wide slices
+    coarse, cent, codes, list_ids, queries = ivf_case(98, 8_003, 48, 16, 70, 40)
+    coarse[7] = coarse[3]
+    coarse[31] = coarse[3]
+    queries[:10] = coarse[3]
+    queries[10:20] = coarse[12]
+    with vk.IVFIndex(coarse, cent, codes, list_ids) as ix:
+        for nprobe in (1, 2, 3):
+            d, i, _ = ix.search(queries, nprobe, 10)
+            assert_same(d, i, orc.ivf_search(coarse, cent, 48, codes, list_ids, queries, nprobe, 10),
+                        f"probe ties nprobe={nprobe}")

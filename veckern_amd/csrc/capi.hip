@@ -801,12 +801,11 @@ struct vk_ivf {
     vk_tuning tuning{};
     vk_launch_shape last{};
     hipStream_t stream = nullptr;
-    DeviceBuffer<float> coarse, centroids, queries, lut;
+    DeviceBuffer<float> coarse, centroids, queries, lut, coarse_dist;
     DeviceBuffer<uint4> codes_v;
     DeviceBuffer<int32_t> ids, slab_list, slab_queries;
     DeviceBuffer<int64_t> list_tile, slab_gran, query_gran;
     DeviceBuffer<Pair> probes, part, out;
-    DeviceBuffer<unsigned> error;
     std::vector<int64_t> list_tile_h;  // [nlist + 1]
 
     ~vk_ivf() {
@@ -821,22 +820,12 @@ struct vk_ivf {
     // d_q: nq x d device queries; d_o: nq x k device results.
     void search(const float* d_q, size_t nq, size_t nprobe, size_t kk, Pair* d_o, vk_timings* t,
                 StageClock& clock) {
-        // 1. the nprobe nearest lists of every query: exact distances to all coarse centroids
+        // 1. the nprobe nearest lists of every query: exact distances to all coarse centroids (a dense tile
+        // kernel), then the nprobe smallest of each row by (dist, list id); in row chunks that keep the distance
+        // matrix within 64 Mi floats
         probes.ensure(nq * nprobe);
-        error.ensure(1);
-        VK_HIP(hipMemsetAsync(error.get(), 0, sizeof(unsigned), stream));
-        vk::RerankArgs pa{};
-        pa.base = coarse.get();
-        pa.n = static_cast<int64_t>(nlist);
-        pa.d = static_cast<int>(d);
-        pa.queries = d_q;
-        pa.nq = static_cast<int64_t>(nq);
-        pa.candidates = nullptr;
-        pa.r = static_cast<int64_t>(nlist);
-        pa.K = vk::plan::dispatched_k(nprobe);
-        pa.k = static_cast<int>(nprobe);
-        pa.out = probes.get();
-        pa.error = error.get();
+        const size_t rows = std::max<size_t>(1, std::min(nq, (size_t{64} << 20) / nlist));
+        coarse_dist.ensure(rows * nlist);
         lut.ensure(nq * m * vk::KSUB);
         // 2. the slab plan, on the device: slabs in query-major order (each query's probed lists in probe order),
         // so a query's slabs are one run of consecutive granules
@@ -848,7 +837,20 @@ struct vk_ivf {
         vk::IvfPlanArgs plan{probes.get(),      static_cast<int>(nprobe), static_cast<int64_t>(nq), list_tile.get(),
                              slab_list.get(),   slab_queries.get(),       slab_gran.get(),           query_gran.get()};
         clock.time(&t->lut_ms, [&] {
-            VK_HIP(vk::launch_rerank(pa, stream));
+            for (size_t r0 = 0; r0 < nq; r0 += rows) {
+                const size_t nr = std::min(rows, nq - r0);
+                VK_HIP(vk::launch_coarse_distances(d_q + r0 * d, static_cast<int64_t>(nr), coarse.get(),
+                                                   static_cast<int64_t>(nlist), static_cast<int>(d), coarse_dist.get(),
+                                                   stream));
+                vk::SelectArgs sel{};
+                sel.mode = 0;
+                sel.dists = coarse_dist.get();
+                sel.len = static_cast<int64_t>(nlist);
+                sel.K = vk::plan::dispatched_k(nprobe);
+                sel.k = static_cast<int>(nprobe);
+                sel.out = probes.get() + r0 * nprobe;
+                VK_HIP(vk::launch_select(sel, static_cast<int>(nr), stream));
+            }
             VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(nq),
                                   1, static_cast<int>(nq), lut.get(), stream));
             VK_HIP(vk::launch_ivf_plan(plan, stream));

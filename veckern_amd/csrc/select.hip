@@ -18,7 +18,7 @@ __global__ void __launch_bounds__(256) select_kernel(SelectArgs a) {
     const int tid = threadIdx.x, lane = __lane_id(), wave = tid / WAVE;
     const int K = a.K;
 
-    WaveList<S> list;
+    WaveList<S, true> list;  // bulk admission: a row's first chunks admit most of their lanes
     list.init();
     if (a.mode == 0) {
         const float* row = a.dists + q * a.len;
