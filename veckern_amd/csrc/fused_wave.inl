@@ -337,17 +337,17 @@ __device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, i
 
 // Final merge of one query of a slab by the last block to finish the slab: the slab's `lists` partial lists for
 // the query (K pairs each, `first[l * K + j]`) are split over the W waves, each streaming its share through a wave
-// list; the W wave lists are then merged by rank into the query's k results. LDS `buf` holds W * K pairs. Called
-// by all threads of the block.
+// list; wave 0 then streams the W wave lists (LDS `buf`, W * K pairs) into the query's k results. Called by all
+// threads of the block.
 template <int S, int W>
 __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K, int k, Pair* out, int shift,
-                                            Pair* buf, int tid, int wave, int lane) {
+                                            Pair* buf, int wave, int lane) {
     WaveList<S, true> wl;
     wl.init();
     stream_pairs(wl, first, wave * 4 * WAVE, W * 4 * WAVE, lists * K, K, lane);
     wl.store(buf + wave * K, K);
     __syncthreads();
-    merge_lists(buf, W, K, out, tid, W * WAVE, k, true, shift);
+    if (wave == 0) merge_query_wave<S>(buf, W, K, k, out, shift, lane);
     __syncthreads();
 }
 
@@ -650,9 +650,13 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
             for (int q = 0; q < QS; ++q) lists[q].store(buf + (q * W + wave) * a.K, a.K);
             __syncthreads();
-#pragma unroll
-            for (int q = 0; q < QS; ++q)
-                merge_lists(buf + q * W * a.K, W, a.K, slab_part + (q * slots + slot) * a.K, tid, T);
+            // Wave q streams query q's W lists (W * K pairs in LDS) into one list (QS <= W).
+            if (wave < QS) {
+                WaveList<S, true> wl;
+                wl.init();
+                stream_pairs(wl, buf + wave * W * a.K, 0, 4 * WAVE, W * a.K, a.K, lane);
+                wl.store(slab_part + (wave * slots + slot) * a.K, a.K);
+            }
         } else {
 #pragma unroll
             for (int q = 0; q < QS; ++q)
@@ -671,15 +675,14 @@ __global__ void __launch_bounds__(T)
         __syncthreads();
         if (last_block) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            if (lpb == W) {  // at most 8 blocks per slab: one wave per query
+            if (lpb == W || QS > 1) {  // one wave per query, the queries in parallel
+                const int per_block = lpb == W ? W : 1;
                 for (int q = wave; q < QS && slab * QS + q < a.nq; q += W)
-                    merge_query_wave<S>(slab_part + q * a.max_slots * W * a.K, count * W, a.K, a.k,
-                                        a.out + (slab * QS + q) * a.k, F16 ? table_shift(qmax[q]) : 0, lane);
-            } else {
-                for (int q = 0; q < QS && slab * QS + q < a.nq; ++q)
-                    merge_query<S, W>(slab_part + q * a.max_slots * a.K, count, a.K, a.k,
-                                      a.out + (slab * QS + q) * a.k, F16 ? table_shift(qmax[q]) : 0, buf, tid,
-                                      wave, lane);
+                    merge_query_wave<S>(slab_part + q * a.max_slots * per_block * a.K, count * per_block, a.K,
+                                        a.k, a.out + (slab * QS + q) * a.k, F16 ? table_shift(qmax[q]) : 0, lane);
+            } else if (slab < static_cast<int64_t>(a.nq)) {  // one query (Q = 1) over many blocks: all waves
+                merge_query<S, W>(slab_part, count, a.K, a.k, a.out + slab * a.k, F16 ? table_shift(qmax[0]) : 0,
+                                  buf, wave, lane);
             }
         }
         item = slab_next;
