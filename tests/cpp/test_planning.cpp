@@ -71,6 +71,9 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
     EXPECT(b.grid == 500 && b.max_slots == 2);
     EXPECT(balanced_partition(1'000'000, 1000, 4, 4, 256, 0, 256).grid == 250);  // one block per slab
     EXPECT(balanced_partition(1'000'000, 1000, 2, 4, 256, 0, 256).grid == 256);  // 500 slabs > 256 slots
+    // small slabs: at least kMinBlockVectors vectors per block (100k vectors = 391 granules of 256: 9 blocks each)
+    EXPECT(balanced_partition(100'000, 100, 4, 4, 512, 0, 256).grid == 25 * 9);
+    EXPECT(balanced_partition(1'000, 1, 1, 4, 512, 0, 256).grid == 1);
     std::mt19937_64 rng(7);
     for (int trial = 0; trial < 300; ++trial) {
         const int64_t n = 1 + static_cast<int64_t>(rng() % 200'000);

@@ -42,11 +42,13 @@ inline int64_t first_block(int64_t item, int64_t grid, int64_t total) { return (
 // Balanced partition of the wave-list scan: slabs of q queries, each cut into granules of 64*ilp vectors;
 // the slabs*n_gran items are split evenly over `grid` blocks. blocks_per_query > 0 fixes the blocks per slab.
 // Otherwise, when the slabs are no more than the resident blocks (`slots`), each slab gets floor(slots / slabs)
-// blocks, at most `cus` (> 0) of them, so that no block crosses a slab boundary; with more slabs than slots,
-// grid = slots and blocks span slab boundaries. Measured on MI355X: with a block per resident slot and ranges
+// blocks, at most `cus` (> 0) of them and each with at least kMinBlockVectors vectors, so that no block crosses a
+// slab boundary; with more slabs than slots, grid = slots and blocks span slab boundaries. Measured on MI355X: with a block per resident slot and ranges
 // crossing slabs, the two blocks sharing a CU finish ~0.4 ms apart at 1M x nq=1000 (the older block's waves get
 // issue priority) and the search takes 1.43 ms; slab-aligned blocks take 1.35 ms (fp16 tables at Q = 8: 1.07 ->
 // 0.90 ms). A slab's blocks beyond one per CU only lengthen its final merge (nq = 1 at 10M: 73 -> 67 us).
+constexpr int64_t kMinBlockVectors = 10240;
+
 struct Partition {
     int64_t slabs = 0, n_gran = 0, total = 0, grid = 0;
     int max_slots = 0;  // most blocks touching one slab = partial lists per query
@@ -64,6 +66,10 @@ inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_
     if (per_slab <= 0 && p.slabs <= slots) {
         per_slab = slots / p.slabs;
         if (cus > 0) per_slab = std::min(per_slab, cus);
+        // At least ~10k vectors per block: below that a block's table build and merges outweigh its scan
+        // (100k vectors, nq=100: 20 blocks per slab 94 us, 10 blocks 78 us).
+        const int64_t min_gran = (kMinBlockVectors + 64 * ilp - 1) / (64 * ilp);
+        per_slab = std::max<int64_t>(1, std::min(per_slab, p.n_gran / min_gran));
     }
     if (per_slab > 0)
         p.grid = p.slabs * std::min<int64_t>(per_slab, p.n_gran);
