@@ -122,6 +122,35 @@ private:
     size_t capacity_ = 0;
 };
 
+// Page-locked host staging (hipHostMalloc): host-buffer searches copy queries in and results out through it, so
+// the transfers are single DMA copies rather than the runtime's chunked pageable path.
+template <typename T>
+class PinnedBuffer {
+public:
+    PinnedBuffer() = default;
+    PinnedBuffer(const PinnedBuffer&) = delete;
+    PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+    ~PinnedBuffer() { release(); }
+    void ensure(size_t count) {
+        if (count <= capacity_) return;
+        release();
+        void* p = nullptr;
+        VK_HIP(hipHostMalloc(&p, std::max<size_t>(count, 1) * sizeof(T), hipHostMallocDefault));
+        ptr_ = static_cast<T*>(p);
+        capacity_ = count;
+    }
+    void release() {
+        if (ptr_) (void)hipHostFree(ptr_);
+        ptr_ = nullptr;
+        capacity_ = 0;
+    }
+    T* get() const { return ptr_; }
+
+private:
+    T* ptr_ = nullptr;
+    size_t capacity_ = 0;
+};
+
 // Event pairs recorded around the stages of one batch; read after the batch's final synchronisation.
 class StageClock {
 public:
@@ -201,6 +230,8 @@ struct vk_searcher {
     DeviceBuffer<uint8_t> codes, codes_il;
     DeviceBuffer<uint4> codes_v;
     DeviceBuffer<Pair> part, out;
+    PinnedBuffer<float> staged_q;     // host-buffer searches: queries and results staged in page-locked memory
+    PinnedBuffer<Pair> staged_out;
     DeviceBuffer<unsigned> counters;
     size_t counters_zeroed = 0;
     bool counters_dirty = false;
@@ -462,17 +493,21 @@ struct vk_searcher {
             const size_t b = std::min(batch, nq - q0);
             queries.ensure(b * d);
             out.ensure(b * kk);
+            staged_q.ensure(b * d);
+            staged_out.ensure(b * kk);
+            std::memcpy(staged_q.get(), host_q + q0 * d, b * d * sizeof(float));
             clock.time(&t->transfer_ms, [&] {
-                VK_HIP(hipMemcpyAsync(queries.get(), host_q + q0 * d, b * d * sizeof(float), hipMemcpyHostToDevice,
+                VK_HIP(hipMemcpyAsync(queries.get(), staged_q.get(), b * d * sizeof(float), hipMemcpyHostToDevice,
                                       stream));
             });
             run_variant(v, queries.get(), b, kk, out.get(), t, clock);
             clock.time(&t->transfer_ms, [&] {
-                VK_HIP(hipMemcpyAsync(host_out + q0 * kk, out.get(), b * kk * sizeof(Pair), hipMemcpyDeviceToHost,
+                VK_HIP(hipMemcpyAsync(staged_out.get(), out.get(), b * kk * sizeof(Pair), hipMemcpyDeviceToHost,
                                       stream));
             });
             clock.settle();
             counters_dirty = false;
+            std::memcpy(host_out + q0 * kk, staged_out.get(), b * kk * sizeof(Pair));
         }
     }
 
@@ -806,6 +841,8 @@ struct vk_ivf {
     DeviceBuffer<int32_t> ids, slab_list, slab_queries;
     DeviceBuffer<int64_t> list_tile, slab_gran, query_gran;
     DeviceBuffer<Pair> probes, part, out;
+    PinnedBuffer<float> staged_q;  // host-buffer searches: queries and results staged in page-locked memory
+    PinnedBuffer<Pair> staged_out;
     std::vector<int64_t> list_tile_h;  // [nlist + 1]
 
     ~vk_ivf() {
@@ -1036,16 +1073,20 @@ VK_EXPORT int vk_ivf_search(vk_ivf* v, const float* queries, size_t nq, size_t n
                 const size_t b = std::min(batch, nq - q0);
                 v->queries.ensure(b * v->d);
                 v->out.ensure(b * k);
+                v->staged_q.ensure(b * v->d);
+                v->staged_out.ensure(b * k);
+                std::memcpy(v->staged_q.get(), queries + q0 * v->d, b * v->d * sizeof(float));
                 clock.time(&t.transfer_ms, [&] {
-                    VK_HIP(hipMemcpyAsync(v->queries.get(), queries + q0 * v->d, b * v->d * sizeof(float),
+                    VK_HIP(hipMemcpyAsync(v->queries.get(), v->staged_q.get(), b * v->d * sizeof(float),
                                           hipMemcpyHostToDevice, v->stream));
                 });
                 v->search(v->queries.get(), b, nprobe, k, v->out.get(), &t, clock);
                 clock.time(&t.transfer_ms, [&] {
-                    VK_HIP(hipMemcpyAsync(out + q0 * k, v->out.get(), b * k * sizeof(Pair), hipMemcpyDeviceToHost,
-                                          v->stream));
+                    VK_HIP(hipMemcpyAsync(v->staged_out.get(), v->out.get(), b * k * sizeof(Pair),
+                                          hipMemcpyDeviceToHost, v->stream));
                 });
                 clock.settle();
+                std::memcpy(out + q0 * k, v->staged_out.get(), b * k * sizeof(Pair));
             }
         }
         if (timings) *timings = t;
