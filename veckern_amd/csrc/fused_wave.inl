@@ -428,9 +428,9 @@ __global__ void __launch_bounds__(T)
     const int64_t start = b * total / grid, end = (b + 1) * total / grid;
     const _Float16 one = opaque_half_one();
 
-    // Inverted lists: the first slab of the block's range by binary search; every later one is the next slab
-    // (slabs are non-empty and contiguous in item order), so the search costs one chain of dependent loads per
-    // block, not one per slab.
+    // Inverted lists: the first slab of the block's range by binary search (the last slab starting at or before
+    // `start`, i.e. the non-empty one holding it); every later one is the next non-empty slab, so the search costs
+    // one chain of dependent loads per block, not one per slab.
     int64_t next_slab = IVF && start < end ? slab_of(a.slab_gran, a.n_slabs, start) : 0;
     // Bulk merges (device.hpp) for long lists, and for inverted lists, whose partial lists cover a few probed lists
     // each, so that many of their candidates arrive while the list is filling. Elsewhere, for K <= 64, their

@@ -5,8 +5,9 @@
 // CPU's, ties included.
 //
 // One lane per (vector, sub-space); a block's lanes share one sub-space (grid y), so the centroid being compared
-// is wave-uniform and is read with scalar loads straight into SGPRs (no LDS staging, no bank conflicts). The
-// 256 x dsub x 3 flops per code are VALU work: about 3 ms for 1M vectors at m=16, d=128. A dense MFMA form
+// is the same for every lane: the sub-space's codebook is staged in LDS once per block and each centroid is an LDS
+// broadcast (scalar loads of it per wave were latency-bound: 26 ms for 1M vectors at m=16, d=128, against ~2.5 ms
+// of VALU work, 256 x dsub x 3 flops per code). A dense MFMA form
 // (|x|^2 - 2 x.c + |c|^2) would be faster but rounds differently and can flip near-ties, so it is not used here.
 #include <cfloat>
 
@@ -30,14 +31,33 @@ __global__ void __launch_bounds__(kAssignThreads) nearest_kernel(NearestArgs a) 
     int best = 0;
     float best_dist = FLT_MAX;
     if constexpr (DSUB > 0) {
+        // The block's sub-space codebook (256 x DSUB floats, <= 16 KB) staged in LDS once; every lane then reads
+        // the same centroid at the same time (an LDS broadcast, 16-byte reads when DSUB % 4 == 0).
+        __shared__ __align__(16) float cl[256 * DSUB];
+        for (int e = threadIdx.x; e < 256 * DSUB; e += kAssignThreads) cl[e] = cent[e];
+        __syncthreads();
         float x[DSUB];
 #pragma unroll
         for (int j = 0; j < DSUB; ++j) x[j] = xr[j];
         for (int c = 0; c < 256; ++c) {
+            float cv[DSUB];
+            if constexpr (DSUB % 4 == 0) {
+#pragma unroll
+                for (int j = 0; j < DSUB; j += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(cl + c * DSUB + j);
+                    cv[j] = v.x;
+                    cv[j + 1] = v.y;
+                    cv[j + 2] = v.z;
+                    cv[j + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < DSUB; ++j) cv[j] = cl[c * DSUB + j];
+            }
             float acc = 0.f;
 #pragma unroll
             for (int j = 0; j < DSUB; ++j) {
-                const float diff = x[j] - cent[c * DSUB + j];
+                const float diff = x[j] - cv[j];
                 acc += diff * diff;
             }
             if (acc < best_dist) {
