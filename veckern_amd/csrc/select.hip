@@ -21,9 +21,29 @@ __global__ void __launch_bounds__(256) select_kernel(SelectArgs a) {
     WaveList<S, true> list;  // bulk admission: a row's first chunks admit most of their lanes
     list.init();
     if (a.mode == 0) {
+        // Rows are long (n distances): each wave reads 4 x 1 KB per round (16-byte loads, four in flight) and
+        // offers them as 16 candidates per lane; the threshold test rejects nearly all of them once the list fills.
         const float* row = a.dists + q * a.len;
-        for (int64_t base = static_cast<int64_t>(wave) * WAVE; base < a.len; base += W * WAVE) {
-            const int64_t j = base + lane;
+        constexpr int R = 4, V = 4, CH = WAVE * V * R;  // floats per wave per round
+        const bool vec = a.len % V == 0 && reinterpret_cast<uintptr_t>(row) % 16 == 0;
+        const int64_t full = vec ? a.len / CH * CH : 0;  // complete rounds; chunk c goes to wave c % W
+        for (int64_t base = static_cast<int64_t>(wave) * CH; base < full; base += W * CH) {
+            float4 v[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                v[r] = *reinterpret_cast<const float4*>(row + base + (r * WAVE + lane) * V);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int32_t j = static_cast<int32_t>(base + (r * WAVE + lane) * V);
+                list.offer(v[r].x, j, true, K);
+                list.offer(v[r].y, j + 1, true, K);
+                list.offer(v[r].z, j + 2, true, K);
+                list.offer(v[r].w, j + 3, true, K);
+            }
+        }
+        // The rest of the row (all of it when unaligned): one distance per lane, waves interleaved.
+        for (int64_t b0 = full + static_cast<int64_t>(wave) * WAVE; b0 < a.len; b0 += W * WAVE) {
+            const int64_t j = b0 + lane;
             const bool valid = j < a.len;
             const float x = valid ? row[j] : INFINITY;
             list.offer(x, static_cast<int32_t>(j), valid, K);
