@@ -261,6 +261,25 @@ struct WaveList {
     }
 };
 
+// Streams pairs [begin, all) of consecutive partial lists through a wave list: four 64-pair chunks per round (four
+// loads in flight), rounds `step` pairs apart so that several waves can split one range. The list takes them with
+// bulk admission (merge_wave): a chunk of sorted partial lists admits many pairs at once while the list fills.
+template <int S>
+__device__ __forceinline__ void stream_pairs(WaveList<S, true>& wl, const Pair* first, int begin, int step, int all,
+                                             int K, int lane) {
+    constexpr int B = 4;
+    for (int base = begin; base < all; base += step) {
+        Pair p[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int e = base + u * WAVE + lane;
+            p[u] = e < all ? first[e] : Pair{INFINITY, kEmptyId};
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) wl.offer(p[u].d, p[u].i, p[u].i != kEmptyId, K);
+    }
+}
+
 // Number of entries of the sorted list l[0..K) that precede e: strictly less when strict, else less-or-equal.
 __device__ __forceinline__ int count_before(const Pair* l, int K, Pair e, bool strict) {
     int lo = 0, hi = K;

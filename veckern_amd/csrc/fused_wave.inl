@@ -301,25 +301,6 @@ __device__ __forceinline__ Pair final_pair(float d, int32_t id, int shift) {
     return Pair{shift ? ldexpf(d, shift) : d, id};
 }
 
-// Streams pairs [begin, all) of consecutive partial lists through a wave list: four 64-pair chunks per round (four
-// loads in flight), rounds `step` pairs apart so that several waves can split one range. The lists are merged with
-// bulk admission (device.hpp): a chunk of sorted partial lists admits many pairs at once while the list fills.
-template <int S>
-__device__ __forceinline__ void stream_pairs(WaveList<S, true>& wl, const Pair* first, int begin, int step, int all,
-                                             int K, int lane) {
-    constexpr int B = 4;
-    for (int base = begin; base < all; base += step) {
-        Pair p[B];
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int e = base + u * WAVE + lane;
-            p[u] = e < all ? first[e] : Pair{INFINITY, kEmptyId};
-        }
-#pragma unroll
-        for (int u = 0; u < B; ++u) wl.offer(p[u].d, p[u].i, p[u].i != kEmptyId, K);
-    }
-}
-
 // Final merge of one query of a slab by a single wave (few partial lists): no barriers; the wave list's first k
 // entries are the results.
 template <int S>
