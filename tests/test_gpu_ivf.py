@@ -154,3 +154,13 @@ def test_ivf_probe_ties_go_to_the_lower_list():
             d, i, _ = ix.search(queries, nprobe, 10)
             assert_same(d, i, orc.ivf_search(coarse, cent, 48, codes, list_ids, queries, nprobe, 10),
                         f"probe ties nprobe={nprobe}")
+
+
+def test_ivf_probe_over_many_lists():
+    # 2,048 coarse centroids: the probe's distance rows are whole 1024-wide rounds of the row select
+    coarse, cent, codes, list_ids, queries = ivf_case(99, 30_011, 32, 16, 45, 2048)
+    with vk.IVFIndex(coarse, cent, codes, list_ids) as ix:
+        for nprobe, k in ((1, 10), (40, 100)):
+            d, i, _ = ix.search(queries, nprobe, k)
+            assert_same(d, i, orc.ivf_search(coarse, cent, 32, codes, list_ids, queries, nprobe, k),
+                        f"nlist=2048 nprobe={nprobe} k={k}")

@@ -146,3 +146,17 @@ def test_tie_heavy_data_every_variant():
                 d, i, _ = s.search(queries, k, v)
                 assert (i == exp["id"]).all() and (d.view(np.uint32) == exp["dist"].view(np.uint32)).all(), \
                     f"{vk.variant_name(v)} k={k}"
+
+
+@pytest.mark.parametrize("n", [12_288, 12_292])
+def test_unfused_selection_on_aligned_rows(n):
+    # rows of n distances with n % 4 == 0: the select kernel reads them in 1024-distance rounds of 16-byte loads
+    # (n = 12,288: whole rounds only; 12,292: a 4-distance tail), k = 10 and 100, ties included
+    centroids, codes, queries = datagen.tie_fixture(n, D, M, 21, seed=23)
+    exp = {k: orc.adc_search(centroids, D, codes, queries, k) for k in (10, 100)}
+    with vk.PQSearcher(centroids, codes, D) as s:
+        for v in SCAN:
+            for k in (10, 100):
+                d, i, _ = s.search(queries, k, v)
+                bad = (i != exp[k]["id"]) | (d.view(np.uint32) != exp[k]["dist"].view(np.uint32))
+                assert not bad.any(), f"{vk.variant_name(v)} n={n} k={k}: {int(bad.sum())} mismatches"
