@@ -126,6 +126,29 @@ def test_ivf_assign_is_the_nearest_coarse_centroid():
     assert (got == exp).all() and (got[:50] == 20).all()
 
 
+@pytest.mark.parametrize("nlist,d,n", [(1, 8, 33), (70, 100, 4_099), (129, 130, 31)])
+def test_ivf_assign_on_ragged_tiles(nlist, d, n):
+    """Centroid counts and dimensions that are not whole 64-wide tiles or slices, fewer vectors than one 32-row
+    tile, duplicated centroids in different tiles (the lower index wins) and a vector of NaNs (list 0)."""
+    rng = np.random.default_rng(nlist * 1000 + d)
+    coarse = rng.standard_normal((nlist, d)).astype(np.float32)
+    if nlist > 65:
+        coarse[nlist - 1] = coarse[3]
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    if nlist > 65:
+        x[: min(n, 7)] = coarse[3]
+    x[n // 2] = np.nan
+    got = vk.ivf_assign(coarse, x)
+    cand = np.zeros((n, nlist), dtype=vk.NEIGHBOR_DTYPE)
+    cand["id"] = np.arange(nlist)
+    exp = orc.rerank_exact(coarse, x, cand, 1)["id"][:, 0]
+    keep = np.arange(n) != n // 2
+    assert (got[keep] == exp[keep]).all()
+    assert got[n // 2] == 0
+    if nlist > 65:
+        assert (got[: min(n, 7)] == 3).all()
+
+
 def test_ivf_device_resident_search_matches_host_buffers(index_case):
     (coarse, cent, codes, list_ids, queries), ix = index_case
     nq, k = queries.shape[0], 10

@@ -1018,26 +1018,19 @@ VK_EXPORT int vk_ivf_assign(const float* coarse, size_t nlist, size_t d, const f
         require(coarse != nullptr && x != nullptr && list_ids != nullptr, "coarse, x and list_ids must not be null");
         PqWorkspace& w = pq_workspace();
         const size_t chunk = std::min(n, encode_chunk(d));
-        DeviceBuffer<unsigned> error;
-        DeviceBuffer<Pair> best;
-        error.ensure(1);
-        best.ensure(chunk);
+        DeviceBuffer<int32_t> ids;
+        ids.ensure(chunk);
         w.centroids.ensure(nlist * d);
         VK_HIP(hipMemcpyAsync(w.centroids.get(), coarse, nlist * d * sizeof(float), hipMemcpyHostToDevice, w.stream));
         w.x.ensure(chunk * d);
-        std::vector<Pair> host(chunk);
         for (size_t i0 = 0; i0 < n; i0 += chunk) {
             const size_t b = std::min(chunk, n - i0);
             VK_HIP(hipMemcpyAsync(w.x.get(), x + i0 * d, b * d * sizeof(float), hipMemcpyHostToDevice, w.stream));
-            VK_HIP(hipMemsetAsync(error.get(), 0, sizeof(unsigned), w.stream));
-            // the nearest coarse centroid of each vector: a re-rank of every centroid, k = 1
-            vk::RerankArgs a{w.centroids.get(), static_cast<int64_t>(nlist), static_cast<int>(d), w.x.get(),
-                             static_cast<int64_t>(b), nullptr, static_cast<int64_t>(nlist), vk::plan::dispatched_k(1),
-                             1, best.get(), error.get()};
-            VK_HIP(vk::launch_rerank(a, w.stream));
-            VK_HIP(hipMemcpyAsync(host.data(), best.get(), b * sizeof(Pair), hipMemcpyDeviceToHost, w.stream));
+            // the nearest coarse centroid of each vector, reduced inside the tiled distance kernel
+            VK_HIP(vk::launch_coarse_assign(w.x.get(), static_cast<int64_t>(b), w.centroids.get(),
+                                            static_cast<int64_t>(nlist), static_cast<int>(d), ids.get(), w.stream));
+            VK_HIP(hipMemcpyAsync(list_ids + i0, ids.get(), b * sizeof(int32_t), hipMemcpyDeviceToHost, w.stream));
             VK_HIP(hipStreamSynchronize(w.stream));
-            for (size_t i = 0; i < b; ++i) list_ids[i0 + i] = host[i].i < 0 ? 0 : host[i].i;
         }
     });
 }

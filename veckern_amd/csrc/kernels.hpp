@@ -83,6 +83,9 @@ hipError_t launch_ivf_plan(const IvfPlanArgs& a, hipStream_t stream);
 // ---- IVF probe (probe.hip): out[q][l] = exact squared L2 distance of query q to coarse centroid l (nq x nlist)
 hipError_t launch_coarse_distances(const float* queries, int64_t nq, const float* coarse, int64_t nlist, int d,
                                    float* out, hipStream_t stream);
+// list_ids[i] = the nearest coarse centroid of vector i by (exact squared L2 distance, centroid index)
+hipError_t launch_coarse_assign(const float* x, int64_t n, const float* coarse, int64_t nlist, int d,
+                                int32_t* list_ids, hipStream_t stream);
 
 // ---- IVF final merge (ivf.hip): block b of the scan (grid blocks, lists_per_block lists of K pairs each) writes
 // its lists for query q at part[(b + q) * lists_per_block * K]; the k results of q go to out[q * k].
