@@ -392,6 +392,7 @@ __global__ void __launch_bounds__(T)
     // filters by it. At K = 128 this removes ~40 % of the inserts; at K <= 64 the bookkeeping costs more than
     // the inserts it saves.
     constexpr bool kShareBound = S > 1;
+    constexpr bool kBulkOne = QS == 1 && !F16;
     __shared__ __align__(16) unsigned rank_bound[QS][W];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
@@ -416,10 +417,18 @@ __global__ void __launch_bounds__(T)
     // Bulk merges (device.hpp) for long lists, and for inverted lists, whose partial lists cover a few probed lists
     // each, so that many of their candidates arrive while the list is filling. Elsewhere, for K <= 64, their
     // registers cost more than they save, and the fp16 kernels (Q = 8) have none to spare.
-    WaveList<S, IVF || (!F16 && S > 1)> lists[QS];
+    WaveList<S, IVF || (!F16 && S > 1) || kBulkOne> lists[QS];
     float published[QS];
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
     int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
+    // One query per block over 16-byte codes: the next granule's code words are loaded before this granule's
+    // lookups (U more registers), so a wave's next memory round trip overlaps its own lookups; a slab's first
+    // granule is loaded before the tables are built. With one query per block the codes stream from HBM and the
+    // few waves per CU leave that latency open otherwise; the multi-query instances read codes mostly from L2 and
+    // need the registers for their accumulators.
+    constexpr bool kPrefetch = !IVF && QS == 1 && M == 16;
+    uint4 next_words[kPrefetch ? U : 1];
+
     for (int64_t item = start; item < end;) {
         // The slab holding `item` and its granules [slab_first, slab_next) in the balanced partition.
         int64_t slab, slab_first, slab_next;
@@ -463,6 +472,13 @@ __global__ void __launch_bounds__(T)
         }
         int64_t list_tile0 = 0;  // IVF: first tile of the slab's list
         if constexpr (IVF) list_tile0 = a.list_tile[a.slab_list[slab]];
+        if constexpr (kPrefetch) {
+            if (g_lo + wave < g_hi) {
+                const uint4* c = a.codes + (g_lo + wave) * U * WAVE + lane;
+#pragma unroll
+                for (int u = 0; u < U; ++u) next_words[u] = c[u * WAVE];
+            }
+        }
 
         if (new_run) {
             __syncthreads();  // the previous slab's merge has finished with LDS
@@ -513,7 +529,16 @@ __global__ void __launch_bounds__(T)
             // count within what the LDS-limited residency allows.
             constexpr int WORDS = M ? M / 16 : 1;
             uint4 cw[U][WORDS];
-            if constexpr (M > 0) {
+            if constexpr (kPrefetch) {
+                const int64_t g_next = g_lo + static_cast<int64_t>(__builtin_amdgcn_readfirstlane(grab));
+#pragma unroll
+                for (int u = 0; u < U; ++u) cw[u][0] = next_words[u];
+                if (g_next < g_hi) {
+                    const uint4* c = a.codes + g_next * U * WAVE + lane;
+#pragma unroll
+                    for (int u = 0; u < U; ++u) next_words[u] = c[u * WAVE];
+                }
+            } else if constexpr (M > 0) {
 #pragma unroll
                 for (int u = 0; u < U; ++u)
 #pragma unroll
