@@ -61,6 +61,24 @@ CASE("blocks_x_fill: ~8 blocks per CU over the grid, >= 16 vectors per thread, o
     EXPECT(blocks_x_fill(10'000'000, 1000, 256, 256, 5) == 5);
 }
 
+CASE("bulk admission is chosen while a block scans few vectors of a slab") {
+    // 100k vectors, nq=100, Q=4: 9 blocks per slab, ~11k vectors each
+    EXPECT(bulk_scan(balanced_partition(100'000, 100, 4, 4, 512, 0, 256), 4));
+    // 10M vectors, nq=8, Q=4: 2 slabs of 256 blocks, ~39k vectors each
+    EXPECT(bulk_scan(balanced_partition(10'000'000, 8, 4, 4, 512, 0, 256), 4));
+    // the 1M headline (2 blocks per slab, 500k vectors each) and 10M at nq=1000 (5M each): one by one
+    EXPECT(!bulk_scan(balanced_partition(1'000'000, 1000, 4, 4, 512, 0, 256), 4));
+    EXPECT(!bulk_scan(balanced_partition(10'000'000, 1000, 4, 4, 512, 0, 256), 4));
+    // the limit: a block's run of one slab, in vectors, against kBulkScanVectors
+    for (int64_t per_block : {int64_t{1000}, int64_t{1023}, int64_t{1024}, int64_t{1025}, int64_t{4096}}) {
+        const int64_t n = per_block * 256 * 4;  // 4 blocks per slab at ilp 1, granules of 64 vectors
+        const Partition p = balanced_partition(n, 8, 4, 1, 8, 4, 0);
+        EXPECT(p.grid == 8);
+        EXPECT(bulk_scan(p, 1) == (per_block * 256 < kBulkScanVectors));
+    }
+    EXPECT(!bulk_scan(Partition{}, 4));
+}
+
 CASE("balanced_partition covers every item exactly once and bounds the slots per slab") {
     // one slab on 256 CUs with two resident blocks each: one block per CU, not two
     EXPECT(balanced_partition(10'000'000, 1, 1, 4, 512, 0, 256).grid == 256);

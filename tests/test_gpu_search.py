@@ -101,6 +101,25 @@ def test_single_query_spreads_over_the_device(fixture, searcher):
     assert s.blocks_x == expected_blocks and s.blocks_x > 1
 
 
+def test_bulk_and_one_by_one_admission_agree():
+    # Blocks that scan few vectors of a slab use the instance admitting candidates in bulk; above 2^18 vectors per
+    # block and slab the one admitting them one by one (the headline's). 300k vectors with one block per slab take
+    # the second, the default spread (~10k vectors per block) the first; both must equal the oracle.
+    n, d, m, nq = 300_007, 64, 16, 9
+    centroids, codes, queries = datagen.random_fixture(n, d, m, nq, seed=41)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        for k in (1, 10, 64):
+            exp = orc.adc_search(centroids, d, codes, queries, k)
+            for q in (2, 4, 8):
+                slabs = -(-nq // q)
+                for bpq in (1, 0):
+                    s.set_tuning(vk.Tuning(queries_per_block=q, blocks_per_query=bpq))
+                    got_d, got_i, _ = s.search(queries, k, vk.ScanVariant.FusedWarp)
+                    assert_same(got_d, got_i, exp, f"k={k} Q={q} bpq={bpq}")
+                    blocks = s.last_launch().blocks_x
+                    assert (blocks == slabs) if bpq == 1 else (blocks > 4 * slabs)
+
+
 @pytest.mark.parametrize("family", ["random", "tie"])
 @pytest.mark.parametrize("m", [16, 32, 64])
 def test_fused_warp_other_m_and_tie_heavy_data(family, m):

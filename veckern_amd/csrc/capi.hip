@@ -22,29 +22,29 @@
 
 namespace vk {
 // Per-m instance tables of the wave-list scan, fp32 (fused_wave_m*.hip) and fp16 tables (fused_wave_h*.hip).
-WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_m64(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_h16(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_h32(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_h64(int qg, int ng, int ilp, int segments);
-WaveScanKernel fused_wave_kernel_hx(int qg, int ng, int ilp, int segments);
+WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_m64(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_h16(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_h32(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_h64(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_hx(int qg, int ng, int ilp, int segments, bool bulk);
 
-WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16) {
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16, bool bulk) {
     if (f16) {
         switch (m) {
-            case 16: return fused_wave_kernel_h16(qg, ng, ilp, segments);
-            case 32: return fused_wave_kernel_h32(qg, ng, ilp, segments);
-            case 64: return fused_wave_kernel_h64(qg, ng, ilp, segments);
-            default: return fused_wave_kernel_hx(qg, ng, ilp, segments);
+            case 16: return fused_wave_kernel_h16(qg, ng, ilp, segments, bulk);
+            case 32: return fused_wave_kernel_h32(qg, ng, ilp, segments, bulk);
+            case 64: return fused_wave_kernel_h64(qg, ng, ilp, segments, bulk);
+            default: return fused_wave_kernel_hx(qg, ng, ilp, segments, bulk);
         }
     }
     switch (m) {
-        case 16: return fused_wave_kernel_m16(qg, ng, ilp, segments);
-        case 32: return fused_wave_kernel_m32(qg, ng, ilp, segments);
-        case 64: return fused_wave_kernel_m64(qg, ng, ilp, segments);
-        default: return fused_wave_kernel_mx(qg, ng, ilp, segments);
+        case 16: return fused_wave_kernel_m16(qg, ng, ilp, segments, bulk);
+        case 32: return fused_wave_kernel_m32(qg, ng, ilp, segments, bulk);
+        case 64: return fused_wave_kernel_m64(qg, ng, ilp, segments, bulk);
+        default: return fused_wave_kernel_mx(qg, ng, ilp, segments, bulk);
     }
 }
 }  // namespace vk
@@ -276,7 +276,7 @@ struct vk_searcher {
         // fp32: 8 queries are two groups of 4 (16-byte reads); fp16: up to 8 queries in one group.
         const int qg = (!f16 && q == 8) ? 4 : q, ng = (!f16 && q == 8) ? 2 : 1;
         const int ilp = tuning.vectors_per_step;
-        const vk::WaveScanKernel kern = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments, f16);
+        vk::WaveScanKernel kern = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments, f16);
         if (!kern.fn) fail(VK_ERR_LOGIC, "no fused-warp kernel built for this (Q, ILP, m, K)");
         const size_t tables = static_cast<size_t>(q) * m * vk::KSUB * entry_bytes;
         require(tables <= info.max_smem_per_block, "LUT does not fit in LDS");
@@ -290,6 +290,19 @@ struct vk_searcher {
         const vk::plan::Partition part_plan = vk::plan::balanced_partition(
             static_cast<int64_t>(n), b, q, ilp, static_cast<int64_t>(per_cu) * info.sm_count, tuning.blocks_per_query,
             info.sm_count);
+        // Few vectors per block: the instance that admits candidates in bulk, if it has the same residency (the
+        // partition above was planned with it).
+        if (!f16 && segments == 1 && q > 1 && vk::plan::bulk_scan(part_plan, ilp)) {
+            const vk::WaveScanKernel bulk = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments, f16, true);
+            int bulk_per_cu = 0;
+            if (bulk.fn) {
+                if (bulk.dynamic_lds)
+                    VK_HIP(hipFuncSetAttribute(bulk.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(smem)));
+                VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&bulk_per_cu, bulk.fn, bulk.threads, smem));
+            }
+            if (bulk.fn && std::max(bulk_per_cu, 1) == per_cu) kern = bulk;
+        }
         // Up to 8 blocks per slab every wave leaves its own partial lists; beyond that the block merges its wave
         // lists first, which keeps the final merge of a slab to at most max(64, blocks per slab) lists per query.
         const int lists_per_block = part_plan.max_slots > 8 ? 1 : kern.threads / vk::WAVE;

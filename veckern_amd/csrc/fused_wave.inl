@@ -364,7 +364,7 @@ __device__ __forceinline__ int64_t slab_of(const int64_t* slab_gran, int64_t sla
 // a.list_tile[list] in the word-interleaved codes, and the vector ids come from a.ids (-1 on padding). A block
 // gathers a query's tables and starts its lists once per run and writes them once, at the end of the run (or of
 // its range); a separate merge kernel combines the partial lists of each query.
-template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF>
+template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF, bool BULK>
 __global__ void __launch_bounds__(T)
     __attribute__((amdgpu_waves_per_eu(wave_kernel_waves_per_simd<QG, NG, M, T, F16>())))
     fused_wave_kernel_t(WaveScanArgs a) {
@@ -414,10 +414,13 @@ __global__ void __launch_bounds__(T)
     // `start`, i.e. the non-empty one holding it); every later one is the next non-empty slab, so the search costs
     // one chain of dependent loads per block, not one per slab.
     int64_t next_slab = IVF && start < end ? slab_of(a.slab_gran, a.n_slabs, start) : 0;
-    // Bulk merges (device.hpp) for long lists, and for inverted lists, whose partial lists cover a few probed lists
-    // each, so that many of their candidates arrive while the list is filling. Elsewhere, for K <= 64, their
-    // registers cost more than they save, and the fp16 kernels (Q = 8) have none to spare.
-    WaveList<S, IVF || (!F16 && S > 1) || kBulkOne> lists[QS];
+    // Bulk admission (device.hpp) for long lists; for inverted lists, whose partial lists cover a few probed lists
+    // each, so that many of their candidates arrive while the list is filling; for one query per block; and where
+    // the launch asks for it (BULK): a list admits about K ln(n / K) candidates over n, a third of the first 64
+    // among them, and one by one those first inserts cost a wave's first step several times a later one. Over a
+    // block's first few steps that dominates; over millions of vectors per block the merge's code in the scan loop
+    // costs about 1 %. The fp16 kernels (Q = 8) have no registers to spare for it.
+    WaveList<S, IVF || (!F16 && S > 1) || kBulkOne || BULK> lists[QS];
     float published[QS];
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
     int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
@@ -695,20 +698,21 @@ __global__ void __launch_bounds__(T)
     }
 }
 
-template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF>
+template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF, bool BULK>
 hipError_t launch_fused_wave_t(const WaveScanArgs& a, int grid, size_t smem, hipStream_t stream) {
-    hipLaunchKernelGGL((fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF>), dim3(grid), dim3(T), smem, stream, a);
+    hipLaunchKernelGGL((fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF, BULK>), dim3(grid), dim3(T), smem, stream,
+                       a);
     return hipGetLastError();
 }
 
-template <int QG, int NG, int U, int M, int S, bool F16, bool IVF = false>
+template <int QG, int NG, int U, int M, int S, bool F16, bool IVF = false, bool BULK = false>
 WaveScanKernel make_wave_kernel() {
     constexpr int T = 512;
     WaveScanKernel k;
-    k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF>);
+    k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF, BULK>);
     k.threads = T;
     k.dynamic_lds = M == 0;
-    k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T, F16, IVF>;
+    k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T, F16, IVF, BULK>;
     return k;
 }
 
@@ -722,14 +726,22 @@ WaveScanKernel select_ivf_kernel(int segments) {
 }
 
 // Instances for one M and entry type: every (QG, NG) whose tables fit in 160 KB of LDS when M is known. fp32
-// tables: QG 1, 2, 4 and two groups of 4; fp16 tables: QG 1, 2, 4, 8 in one group.
+// tables: QG 1, 2, 4 and two groups of 4; fp16 tables: QG 1, 2, 4, 8 in one group. `bulk` asks for bulk admission
+// into one-register lists: a second instance of the fp32 multi-query kernels (the others admit in bulk already, or,
+// fp16, never); an empty result when there is none.
 template <int M, bool F16>
-WaveScanKernel select_wave_kernel(int qg, int ng, int ilp, int segments) {
+WaveScanKernel select_wave_kernel(int qg, int ng, int ilp, int segments, bool bulk) {
     constexpr int kLds = 160 * 1024;
 #define VK_WAVE_CASE(QG_, NG_)                                                                      \
     if (qg == QG_ && ng == NG_) {                                                                   \
         if constexpr (M == 0 || NG_ * M * KSUB * Entries<QG_, F16>::kBytes <= kLds) {               \
-            if (segments == 1) {                                                                    \
+            if (segments == 1 && bulk) {                                                            \
+                if constexpr (!F16 && QG_ * NG_ > 1) {                                              \
+                    if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 1, F16, false, true>();   \
+                    if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 1, F16, false, true>();   \
+                    if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 1, F16, false, true>();   \
+                }                                                                                   \
+            } else if (segments == 1) {                                                             \
                 if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 1, F16>();                    \
                 if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 1, F16>();                    \
                 if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 1, F16>();                    \

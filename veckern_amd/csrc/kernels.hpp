@@ -59,8 +59,9 @@ struct WaveScanKernel {
     hipError_t (*launch)(const WaveScanArgs&, int grid, size_t smem, hipStream_t) = nullptr;
 };
 
-// Returns a kernel with fn == nullptr when the combination is not built. f16: binary16 tables (v9).
-WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16);
+// Returns a kernel with fn == nullptr when the combination is not built. f16: binary16 tables (v9). bulk: the
+// instance with bulk admission into one-register lists (fp32, more than one query per block only).
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16, bool bulk = false);
 // The inverted-list scan (ivf_m*.hip): fp32 tables, one query per slab, four tiles per wave step.
 WaveScanKernel ivf_kernel(int m, int segments);
 

@@ -86,6 +86,19 @@ inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_
     return p;
 }
 
+// Bulk admission into one-register wave lists pays while a block scans few vectors of a slab: it replaces the
+// one-by-one inserts into the fresh lists of a block's first steps (several times the cost of a later step),
+// and over millions of vectors per block its code in the scan loop costs about 1 %. Measured with 4 queries per
+// block: 11k vectors per block -26 %, 39k -11 %, 500k neutral, 5M +1 %.
+constexpr int64_t kBulkScanVectors = int64_t{1} << 18;
+
+// Vectors one block scans of one slab (the longest run of a slab's granules in one block) below the bulk limit.
+inline bool bulk_scan(const Partition& p, int ilp) {
+    if (p.grid <= 0 || p.total <= 0) return false;
+    const int64_t per_block = std::min(p.n_gran, (p.total + p.grid - 1) / p.grid);
+    return per_block * 64 * ilp < kBulkScanVectors;
+}
+
 // blocks_x of the unfused scans and v4 (searcher.cu:172-177): an override, else about 8 blocks per CU over the
 // whole grid, never fewer than 16 vectors per thread.
 inline int64_t blocks_x_fill(int64_t n, int64_t grid_y, int threads, int cus, int blocks_per_query) {
