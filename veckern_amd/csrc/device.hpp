@@ -232,6 +232,39 @@ struct WaveList {
         const bool less = (cd < d[S - 1]) | ((cd == d[S - 1]) & (ci < id[S - 1]));
         d[S - 1] = less ? cd : d[S - 1];
         id[S - 1] = less ? ci : id[S - 1];
+        clean(K);
+    }
+
+    // Lists with at least this many admitted entries are merged whole rather than inserted one by one.
+    static constexpr int kListMergeMin = 3;
+
+    // Admits a whole sorted list given in descending order over the 64*S positions: position p holds the list's
+    // entry 64*S-1-p, or the empty slot where the list has none (a list of K entries fills the last K positions).
+    // A few admitted entries go in one by one. More go in by one bitonic merge: the elementwise minimum of the
+    // ascending list and the descending one is a bitonic sequence holding the 64*S smallest pairs of both, which
+    // the clean sorts; no sort of the incoming list is needed.
+    __device__ __forceinline__ void admit_desc(float (&cd)[S], int32_t (&ci)[S], int K) {
+        int admitted = 0;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            admitted += __popcll(__builtin_amdgcn_ballot_w64((cd[s] <= filter) & (ci[s] != kEmptyId)));
+        if (admitted == 0) return;
+        if (admitted < kListMergeMin) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) offer(cd[s], ci[s], ci[s] != kEmptyId, K);
+            return;
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const bool less = (cd[s] < d[s]) | ((cd[s] == d[s]) & (ci[s] < id[s]));
+            d[s] = less ? cd[s] : d[s];
+            id[s] = less ? ci[s] : id[s];
+        }
+        clean(K);
+    }
+
+    // Sorts the list after an elementwise minimum left it bitonic, and reads the new threshold.
+    __device__ __forceinline__ void clean(int K) {
 #pragma unroll
         for (int h = S / 2; h > 0; h >>= 1)  // register distances (S is a power of two)
 #pragma unroll
@@ -278,6 +311,56 @@ __device__ __forceinline__ void stream_pairs(WaveList<S, true>& wl, const Pair* 
 #pragma unroll
         for (int u = 0; u < B; ++u) wl.offer(p[u].d, p[u].i, p[u].i != kEmptyId, K);
     }
+}
+
+// Streams whole partial lists [begin, lists), `step` lists apart, through a wave list: each sorted list of K
+// pairs is read into the wave list's layout in descending order and admitted by `admit_desc`, with the next four
+// lists' loads in flight. For long lists (K > 32): after the first few, a list still admits about K / j of its
+// entries at the j-th, which one by one cost far more than one merge network.
+template <int S>
+__device__ __forceinline__ void stream_lists(WaveList<S, true>& wl, const Pair* first, int begin, int step,
+                                             int lists, int K, int lane) {
+    constexpr int L = 4;
+    float rd[L][S];
+    int32_t ri[L][S];
+    auto load = [&](int l, float (&dd)[S], int32_t (&ii)[S]) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int j = S * WAVE - 1 - (s * WAVE + lane);  // the list's entry at this position
+            const bool have = l < lists && j < K;
+            const Pair e = have ? first[static_cast<int64_t>(l) * K + j] : Pair{INFINITY, kEmptyId};
+            dd[s] = e.d;
+            ii[s] = e.i;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < L; ++u) load(begin + u * step, rd[u], ri[u]);
+    for (int l0 = begin; l0 < lists; l0 += L * step) {
+#pragma unroll
+        for (int u = 0; u < L; ++u) {
+            const int l = l0 + u * step;
+            if (l >= lists) break;
+            float cd[S];
+            int32_t ci[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                cd[s] = rd[u][s];
+                ci[s] = ri[u][s];
+            }
+            load(l + L * step, rd[u], ri[u]);
+            wl.admit_desc(cd, ci, K);
+        }
+    }
+}
+
+// Merges share `part` of `parts` (waves splitting one merge) of `lists` consecutive partial lists of K sorted pairs
+// into a wave list: whole lists, every parts-th, when they are long; else rounds of four 64-pair chunks, every
+// parts-th round (several short lists per ballot).
+template <int S>
+__device__ __forceinline__ void stream_partials(WaveList<S, true>& wl, const Pair* first, int part, int parts,
+                                                int lists, int K, int lane) {
+    if (K > 32) stream_lists(wl, first, part, parts, lists, K, lane);
+    else stream_pairs(wl, first, part * 4 * WAVE, parts * 4 * WAVE, lists * K, K, lane);
 }
 
 // Number of entries of the sorted list l[0..K) that precede e: strictly less when strict, else less-or-equal.

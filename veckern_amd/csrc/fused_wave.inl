@@ -308,7 +308,7 @@ __device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, i
                                                  int lane) {
     WaveList<S, true> wl;
     wl.init();
-    stream_pairs(wl, first, 0, 4 * WAVE, lists * K, K, lane);
+    stream_partials(wl, first, 0, 1, lists, K, lane);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int j = s * WAVE + lane;
@@ -325,7 +325,7 @@ __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K,
                                             Pair* buf, int wave, int lane) {
     WaveList<S, true> wl;
     wl.init();
-    stream_pairs(wl, first, wave * 4 * WAVE, W * 4 * WAVE, lists * K, K, lane);
+    stream_partials(wl, first, wave, W, lists, K, lane);
     wl.store(buf + wave * K, K);
     __syncthreads();
     if (wave == 0) merge_query_wave<S>(buf, W, K, k, out, shift, lane);
@@ -663,7 +663,7 @@ __global__ void __launch_bounds__(T)
             if (wave < QS) {
                 WaveList<S, true> wl;
                 wl.init();
-                stream_pairs(wl, buf + wave * W * a.K, 0, 4 * WAVE, W * a.K, a.K, lane);
+                stream_partials(wl, buf + wave * W * a.K, 0, 1, W, a.K, lane);
                 wl.store(slab_part + (wave * slots + slot) * a.K, a.K);
             }
         } else {

@@ -99,8 +99,8 @@ __global__ void __launch_bounds__(kPlanThreads) ivf_plan_offsets_kernel(IvfPlanA
     if (s == slabs) a.slab_gran[s] = a.query_gran[a.nq];
 }
 
-// One wave per query streams the pairs of its partial lists through a wave list (four 64-pair chunks in flight
-// per round) and writes the k best, empty slots as {+inf, -1}. The lists of query q are those of the blocks
+// One wave per query streams its partial lists through a wave list (device.hpp: whole lists when long, else
+// 64-pair chunks) and writes the k best, empty slots as {+inf, -1}. The lists of query q are those of the blocks
 // b_lo .. b_hi that cover its run, at (b + q) * W * K (the scan's layout), so one contiguous range; the scan used
 // min(grid, total) blocks, each owning at least one granule, so every block of that range wrote its lists.
 template <int S>
@@ -109,27 +109,15 @@ __global__ void __launch_bounds__(kMergeThreads) ivf_merge_kernel(IvfMergeArgs a
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / WAVE);
     const int64_t q = static_cast<int64_t>(blockIdx.x) * (kMergeThreads / WAVE) + wave;
     if (q >= a.nq) return;  // wave-uniform
-    WaveList<S> wl;
+    WaveList<S, true> wl;
     wl.init();
     const int64_t r_first = a.query_gran[q], r_next = a.query_gran[q + 1], total = a.query_gran[a.nq];
     const int64_t grid = min(a.grid, total);  // the blocks that took part in the scan
-    int64_t len = 0;
-    const Pair* first = a.part;
     if (r_next > r_first) {  // an empty run (no probed vectors) has no lists: all slots stay empty
         const int64_t b_lo = first_block_of(r_first, grid, total), b_hi = first_block_of(r_next - 1, grid, total);
-        first = a.part + (b_lo + q) * a.lists_per_block * a.K;
-        len = (b_hi - b_lo + 1) * a.lists_per_block * a.K;
-    }
-    constexpr int B = 4;
-    for (int64_t base = 0; base < len; base += B * WAVE) {
-        Pair e[B];
-#pragma unroll
-        for (int u = 0; u < B; ++u) {
-            const int64_t j = base + u * WAVE + lane;
-            e[u] = j < len ? first[j] : Pair{INFINITY, kEmptyId};
-        }
-#pragma unroll
-        for (int u = 0; u < B; ++u) wl.offer(e[u].d, e[u].i, e[u].i != kEmptyId, a.K);
+        const Pair* first = a.part + (b_lo + q) * a.lists_per_block * a.K;
+        const int lists = static_cast<int>((b_hi - b_lo + 1) * a.lists_per_block);
+        stream_partials(wl, first, 0, 1, lists, a.K, lane);
     }
     Pair* out = a.out + q * a.k;
 #pragma unroll
