@@ -101,6 +101,27 @@ def test_single_query_spreads_over_the_device(fixture, searcher):
     assert s.blocks_x == expected_blocks and s.blocks_x > 1
 
 
+@pytest.mark.parametrize("family", ["random", "tie"])
+def test_long_lists_merge_whole(family):
+    # One query over ~20 blocks: each block merges its 8 wave lists, and the last block's 8 waves split the blocks'
+    # lists; lists longer than 32 go in whole through the bitonic list merge, shorter ones as 64-pair chunks.
+    # k on both sides of 32 and of 64 (one and two list registers); tie-heavy data exercises the id order.
+    gen = datagen.random_fixture if family == "random" else datagen.tie_fixture
+    n, d, m, nq = 200_003, 32, 16, 3
+    centroids, codes, queries = gen(n, d, m, nq, seed=23)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        s.set_tuning(vk.Tuning(queries_per_block=1))
+        for k in (32, 33, 64, 65, 100, 128):
+            got_d, got_i, _ = s.search(queries[:1], k, vk.ScanVariant.FusedWarp)
+            assert s.last_launch().blocks_x > 8
+            assert_same(got_d, got_i, orc.adc_search(centroids, d, codes, queries[:1], k), f"{family} nq=1 k={k}")
+            # the three queries in one slab over 3 blocks: a wave of the last block merges each query's 24 lists
+            s.set_tuning(vk.Tuning(queries_per_block=4, blocks_per_query=3))
+            got_d, got_i, _ = s.search(queries, k, vk.ScanVariant.FusedWarp)
+            assert_same(got_d, got_i, orc.adc_search(centroids, d, codes, queries, k), f"{family} Q=4 k={k}")
+            s.set_tuning(vk.Tuning(queries_per_block=1))
+
+
 def test_bulk_and_one_by_one_admission_agree():
     # Blocks that scan few vectors of a slab use the instance admitting candidates in bulk; above 2^18 vectors per
     # block and slab the one admitting them one by one (the headline's). 300k vectors with one block per slab take
