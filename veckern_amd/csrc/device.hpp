@@ -216,6 +216,16 @@ struct WaveList {
         }
     }
 
+    // As offer_masked, with bulk admission whatever BULK is (a list's first candidates).
+    __device__ __forceinline__ void offer_masked_bulk(float x, int32_t xi, uint64_t valid, int K) {
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(x <= filter) & valid;
+        if (__popcll(mask) >= kMergeMin) {
+            merge_wave(x, xi, (mask >> __lane_id()) & 1, K);
+            return;
+        }
+        offer_masked(x, xi, valid, K);
+    }
+
     // Admitted lanes from which one bitonic merge of the whole wave costs less than inserting them one by one.
     // BULK = false inserts one by one always: by default for single-register lists (K <= 64), where the merge's
     // code and registers cost the scan loop more than the inserts it replaces.

@@ -509,7 +509,10 @@ __global__ void __launch_bounds__(T)
         }
         const uint32_t n32 = static_cast<uint32_t>(a.n);  // n < 2^31: ids and tile bounds fit in 32 bits
 
-        for (int64_t g = g_lo + wave; g < g_hi;) {
+        // One granule step of this wave (g: the wave's granule, advanced at the end). bulk_step: candidates are
+        // admitted in bulk whatever the list type.
+        int64_t g = g_lo + wave;
+        auto granule = [&](auto bulk_step) __attribute__((always_inline)) {
             // The next granule for this wave, asked for now and used after this one (inverted lists: every W-th).
             unsigned grab = 0;
             if constexpr (!IVF)
@@ -616,7 +619,10 @@ __global__ void __launch_bounds__(T)
                     valid = first + WAVE <= n32 ? ~uint64_t{0} : __builtin_amdgcn_ballot_w64(id < n32);
                 }
 #pragma unroll
-                for (int q = 0; q < QS; ++q) lists[q].offer_masked(acc[q], static_cast<int32_t>(id), valid, a.K);
+                for (int q = 0; q < QS; ++q) {
+                    if constexpr (decltype(bulk_step)::value) lists[q].offer_masked_bulk(acc[q], static_cast<int32_t>(id), valid, a.K);
+                    else lists[q].offer_masked(acc[q], static_cast<int32_t>(id), valid, a.K);
+                }
             }
             // Publish this wave's entry ceil(K/W) - 1 when it has fallen.
             if constexpr (kShareBound) {
@@ -631,7 +637,16 @@ __global__ void __launch_bounds__(T)
             }
             if constexpr (IVF) g += W;
             else g = g_lo + static_cast<int64_t>(__builtin_amdgcn_readfirstlane(grab));
+        };
+        // Lists that admit one by one take a wave's first step in bulk: the fresh lists admit about a third of the
+        // first tile's candidates and, one by one, those inserts made the step several times a later one, with
+        // every wave of the CU inserting at once. The step is a separate copy of the body ahead of the loop, so the
+        // loop's own code is that of one-by-one admission (1M x nq=1000: -1.4 %).
+        constexpr bool kPeel = !F16 && !(IVF || S > 1 || kBulkOne || BULK);
+        if constexpr (kPeel) {
+            if (g < g_hi) granule(std::true_type{});
         }
+        while (g < g_hi) granule(std::false_type{});
 
         // Inverted lists: when the query's run of slabs ends (or the block's range does), every wave writes its
         // list for the query at part[((b + query) * W + wave) * K]. Along the granule order both the block and the
