@@ -641,8 +641,8 @@ __global__ void __launch_bounds__(T)
         // Lists that admit one by one take a wave's first step in bulk: the fresh lists admit about a third of the
         // first tile's candidates and, one by one, those inserts made the step several times a later one, with
         // every wave of the CU inserting at once. The step is a separate copy of the body ahead of the loop, so the
-        // loop's own code is that of one-by-one admission (1M x nq=1000: -1.4 %).
-        constexpr bool kPeel = !F16 && !(IVF || S > 1 || kBulkOne || BULK);
+        // loop's own code is that of one-by-one admission (1M x nq=1000: -1.2 %; fp16 tables, 8 queries: -5 %).
+        constexpr bool kPeel = !(IVF || S > 1 || kBulkOne || BULK);
         if constexpr (kPeel) {
             if (g < g_hi) granule(std::true_type{});
         }
