@@ -170,6 +170,7 @@ def bench_ivf(args, centroids, codes, queries, base):
     elapsed = time.perf_counter() - t0
     qps = nq * args.steps / elapsed
     res = dout.download(np.empty((nq, k), dtype=vk.NEIGHBOR_DTYPE))
+    ix.search(queries, nprobe, k)  # untimed: the first host-buffer search allocates the page-locked staging
     t0 = time.perf_counter()
     for _ in range(args.steps):
         dist, ids_out, t = ix.search(queries, nprobe, k)
