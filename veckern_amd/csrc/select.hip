@@ -6,6 +6,8 @@
 //   mode 1 — bx partial K-lists per query laid out [q][bx][K] (per-thread-list fused scans).
 // Empty slots ({+inf, INT32_MAX}) are skipped, like the reference skips id < 0, and the output turns any that
 // remain into {+inf, -1}.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace vk {
@@ -21,26 +23,34 @@ __global__ void __launch_bounds__(256) select_kernel(SelectArgs a) {
     WaveList<S, true> list;  // bulk admission: a row's first chunks admit most of their lanes
     list.init();
     if (a.mode == 0) {
-        // Rows are long (n distances): each wave reads 4 x 1 KB per round (16-byte loads, four in flight) and
-        // offers them as 16 candidates per lane; the threshold test rejects nearly all of them once the list fills.
+        // Long rows (n distances of an unfused scan): each wave reads 4 x 1 KB per round (16-byte loads, four in
+        // flight) and offers them as 16 candidates per lane; the threshold test rejects nearly all of them once the
+        // list fills. Short rows (an IVF probe's nlist distances): one 16-byte load per lane per round, so that
+        // every wave of the block takes a share of the row.
         const float* row = a.dists + q * a.len;
-        constexpr int R = 4, V = 4, CH = WAVE * V * R;  // floats per wave per round
+        constexpr int V = 4;
         const bool vec = a.len % V == 0 && reinterpret_cast<uintptr_t>(row) % 16 == 0;
-        const int64_t full = vec ? a.len / CH * CH : 0;  // complete rounds; chunk c goes to wave c % W
-        for (int64_t base = static_cast<int64_t>(wave) * CH; base < full; base += W * CH) {
-            float4 v[R];
+        auto rounds = [&](auto r_tag) -> int64_t {
+            constexpr int R = decltype(r_tag)::value, CH = WAVE * V * R;  // floats per wave per round
+            const int64_t full = vec ? a.len / CH * CH : 0;  // complete rounds; chunk c goes to wave c % W
+            for (int64_t base = static_cast<int64_t>(wave) * CH; base < full; base += W * CH) {
+                float4 v[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                v[r] = *reinterpret_cast<const float4*>(row + base + (r * WAVE + lane) * V);
+                for (int r = 0; r < R; ++r)
+                    v[r] = *reinterpret_cast<const float4*>(row + base + (r * WAVE + lane) * V);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int32_t j = static_cast<int32_t>(base + (r * WAVE + lane) * V);
-                list.offer(v[r].x, j, true, K);
-                list.offer(v[r].y, j + 1, true, K);
-                list.offer(v[r].z, j + 2, true, K);
-                list.offer(v[r].w, j + 3, true, K);
+                for (int r = 0; r < R; ++r) {
+                    const int32_t j = static_cast<int32_t>(base + (r * WAVE + lane) * V);
+                    list.offer(v[r].x, j, true, K);
+                    list.offer(v[r].y, j + 1, true, K);
+                    list.offer(v[r].z, j + 2, true, K);
+                    list.offer(v[r].w, j + 3, true, K);
+                }
             }
-        }
+            return full;
+        };
+        const int64_t full = a.len >= int64_t{W} * WAVE * V * 4 ? rounds(std::integral_constant<int, 4>{})
+                                                                 : rounds(std::integral_constant<int, 1>{});
         // The rest of the row (all of it when unaligned): one distance per lane, waves interleaved.
         for (int64_t b0 = full + static_cast<int64_t>(wave) * WAVE; b0 < a.len; b0 += W * WAVE) {
             const int64_t j = b0 + lane;
