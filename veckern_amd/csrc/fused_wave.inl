@@ -566,24 +566,30 @@ __global__ void __launch_bounds__(T)
                 auto lookup_word = [&](const uint4 word, const int w) {
                     const uint32_t part[4] = {word.x, word.y, word.z, word.w};
                     if constexpr (F16 && QG >= 4) {
-                        // The word's reads are all issued before its accumulations: the one-statement-per-read
-                        // accumulations would otherwise be scheduled right behind their own read, one read in
-                        // flight at a time.
-                        V v[16 * NG];
+                        // The word's reads are issued eight at a time before their accumulations: the
+                        // one-statement-per-read accumulations would otherwise be scheduled right behind their own
+                        // read, one read in flight at a time. Eight, not all sixteen: the sixteen results held 64
+                        // VGPRs and made the 8-query loop reload spilled values every step (8 queries: 1M -0.8 %,
+                        // 10M -1.4 %).
 #pragma unroll
-                        for (int j = 0; j < 16; ++j) {
-                            const uint32_t c = (part[j >> 2] >> (8 * (j & 3))) & 0xffu;
-                            const int s = w * 16 + j;
+                        for (int h = 0; h < 2; ++h) {
+                            V v[8 * NG];
 #pragma unroll
-                            for (int t = 0; t < NG; ++t)
-                                v[j * NG + t] = *reinterpret_cast<const V*>(
-                                    tables + t * table_bytes + (s * KSUB + static_cast<int>(c)) * E::kBytes);
+                            for (int jj = 0; jj < 8; ++jj) {
+                                const int j = h * 8 + jj;
+                                const uint32_t c = (part[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                                const int s = w * 16 + j;
+#pragma unroll
+                                for (int t = 0; t < NG; ++t)
+                                    v[jj * NG + t] = *reinterpret_cast<const V*>(
+                                        tables + t * table_bytes + (s * KSUB + static_cast<int>(c)) * E::kBytes);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                                for (int t = 0; t < NG; ++t) E::add(&acc[t * QG], v[jj * NG + t], one);
                         }
-                        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                        for (int j = 0; j < 16; ++j)
-#pragma unroll
-                            for (int t = 0; t < NG; ++t) E::add(&acc[t * QG], v[j * NG + t], one);
                         return;
                     }
 #pragma unroll
