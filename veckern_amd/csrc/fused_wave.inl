@@ -392,7 +392,6 @@ __global__ void __launch_bounds__(T)
     // filters by it. At K = 128 this removes ~40 % of the inserts; at K <= 64 the bookkeeping costs more than
     // the inserts it saves.
     constexpr bool kShareBound = S > 1;
-    constexpr bool kBulkOne = QS == 1 && !F16;
     __shared__ __align__(16) unsigned rank_bound[QS][W];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
@@ -419,7 +418,9 @@ __global__ void __launch_bounds__(T)
     // the launch asks for it (BULK): a list admits about K ln(n / K) candidates over n, a third of the first 64
     // among them, and one by one those first inserts cost a wave's first step several times a later one. Over a
     // block's first few steps that dominates; over millions of vectors per block the merge's code in the scan loop
-    // costs about 1 %. The fp16 kernels (Q = 8) have no registers to spare for it.
+    // costs about 1 %. The fp16 kernels (Q = 8) have no registers to spare for it in the loop. Lists that admit
+    // one by one still take a wave's first granule step in bulk (kPeel, at the scan loop).
+    constexpr bool kBulkOne = QS == 1 && !F16;
     WaveList<S, IVF || (!F16 && S > 1) || kBulkOne || BULK> lists[QS];
     float published[QS];
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
