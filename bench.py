@@ -234,7 +234,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="B", choices=sorted(CONFIGS))
     ap.add_argument("--variant", default="v8")
-    ap.add_argument("--queries-per-block", type=int, default=4)
+    ap.add_argument("--queries-per-block", type=int, default=None,
+                    help="Q (default 2 for config A, whose 100k-vector slabs give a block too little to scan for "
+                         "4 queries' tables; 4 otherwise)")
     ap.add_argument("--ilp", type=int, default=4)
     ap.add_argument("--blocks-per-query", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and its parity check")
@@ -275,6 +277,8 @@ def main():
         + f"; HBM read {hbm_gbs:.0f} GB/s")
 
     s = vk.PQSearcher(centroids, codes, d)
+    if args.queries_per_block is None:
+        args.queries_per_block = 2 if args.config == "A" else 4
     s.set_tuning(vk.Tuning(queries_per_block=args.queries_per_block, vectors_per_step=args.ilp,
                            blocks_per_query=args.blocks_per_query))
     dq = vk.DeviceArray.from_host(queries)
