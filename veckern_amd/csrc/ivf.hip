@@ -1,5 +1,5 @@
 // Inverted-file (IVF) search, the reference's "coarse partitioning" next step (README.md:219): per query, the
-// nprobe nearest coarse centroids (exact distances, the re-rank kernel with every list as a candidate), then the
+// nprobe nearest coarse centroids (exact distances in tiles, probe.hip, and the row top-k of select.hip), then the
 // fused wave-list scan over only those lists' PQ codes (fused_wave.inl with IVF = true: slabs = (query, probed
 // list) in query-major order), then this file's merge of each query's partial lists. The slab plan is built on
 // the device from the probes (this file's plan kernels), so a search makes no host round trip before its results.
