@@ -111,16 +111,23 @@ def cpu_baseline(centroids, codes, queries, k, d, target_s=10.0):
     run(queries[:probe])
     per_query = (time.perf_counter() - t0) / probe
     sample = int(min(nq, max(probe, round(target_s / max(per_query, 1e-9)))))
+    # When the whole batch takes well under that, passes over it are repeated until about 2 s of wall time (some
+    # 30 s of CPU work on 16 threads), a steadier rate than one short pass; otherwise one pass over the sample.
     t0 = time.perf_counter()
     res = run(queries[:sample])
+    passes = 1
+    while sample == nq and time.perf_counter() - t0 < 2.0:
+        run(queries)
+        passes += 1
     elapsed = time.perf_counter() - t0
     rec = {
-        "value": sample / elapsed,
+        "value": sample * passes / elapsed,
         "unit": "queries/s",
         "cores": cores,
         "kind": "reference" if use_ref else "port",
         "sample": f"first {sample} of the {nq} queries against all {codes.shape[0]} codes, k={k}, "
-                  f"{elapsed:.2f} s wall on {cores} OpenMP threads "
+                  + (f"{passes} passes, " if passes > 1 else "")
+                  + f"{elapsed:.2f} s wall on {cores} OpenMP threads "
                   + ("(reference src/cpu/cpu_ref.cpp adc_search, -O3 -fopenmp)" if use_ref
                      else "(oracle port of cpu_ref.cpp adc_search, -O3 -fopenmp)"),
     }
