@@ -67,9 +67,8 @@ void check_search(std::size_t k, ScanVariant v, const gpu::Tuning& tuning = {}) 
 
 const ScanVariant kScans[] = {ScanVariant::GlobalLut, ScanVariant::SharedLut, ScanVariant::SharedLutVec,
                               ScanVariant::Interleaved};
-// v4 is rejected before launch in this build (see the case "v4 is rejected").
-const ScanVariant kFused[] = {ScanVariant::FusedReg, ScanVariant::FusedVec, ScanVariant::FusedVecMQ,
-                              ScanVariant::FusedWarp};
+const ScanVariant kFused[] = {ScanVariant::Fused, ScanVariant::FusedReg, ScanVariant::FusedVec,
+                              ScanVariant::FusedVecMQ, ScanVariant::FusedWarp};
 
 }  // namespace
 
@@ -155,10 +154,10 @@ CASE("launch shape is reported and a single query fills the device") {
     searcher.search(f.queries.data(), 1, 10, ScanVariant::FusedWarp, one.data());
     const auto single = searcher.last_launch();
     std::printf("      v8, 1 query: blocks=%d waves=%.2f\n", single.blocks_x, single.waves);
-    // One query is spread over the device: a block per ~10k vectors (40 granules of 256), at most one per CU.
+    // One query is spread over ceil(n / (16 vectors x 512 threads)) blocks (the reference's rule, test_gpu.cpp:139-145),
+    // at most one per CU.
     const auto info = gpu::device_info();
-    const double granules = std::ceil(static_cast<double>(f.n) / 256.0);
-    const double expected = std::min<double>(info.sm_count, std::max(1.0, std::floor(granules / 40.0)));
+    const std::size_t expected = std::min<std::size_t>(info.sm_count, (f.n + 8191) / 8192);
     EXPECT(single.blocks_x == static_cast<int>(expected) && single.blocks_x > 1);
 }
 
@@ -176,17 +175,14 @@ CASE("word-interleaved variants reject m % 16 != 0; v5 accepts it") {
     same(got, oracle_search(pq8, codes8, f.n, f.queries.data(), f.nq, 10), "v5 m=8");
 }
 
-CASE("v4 is rejected before launch with std::logic_error") {
+CASE("v4 reports the reference's launch shape: one query per block row, blocks_x from the fill rule") {
     auto& f = fixture();
     gpu::PQSearcher searcher(f.pq, f.codes.data(), f.n);
-    std::vector<Neighbor> out(10);
-    bool logic = false;
-    try {
-        searcher.search(f.queries.data(), 1, 10, ScanVariant::Fused, out.data());
-    } catch (const std::logic_error&) {
-        logic = true;
-    }
-    EXPECT(logic);
+    std::vector<Neighbor> out(f.nq * 10);
+    searcher.search(f.queries.data(), f.nq, 10, ScanVariant::Fused, out.data());
+    const auto shape = searcher.last_launch();
+    EXPECT(shape.grid_y == static_cast<int>(f.nq) && shape.queries_per_block == 1 && shape.threads == 256);
+    EXPECT(shape.blocks_x >= 1);
 }
 
 CASE("invalid tuning is rejected") {

@@ -263,63 +263,79 @@ struct vk_searcher {
         VK_HIP(hipStreamSynchronize(stream));
     }
 
-    // v8 / v9 (f16 tables): the wave-list scan over the balanced partition with its final merge, one launch.
-    // d_q: device queries of this batch; writes b x kk results to d_out.
-    void run_wave(const float* d_q, size_t b, size_t kk, bool f16, Pair* d_out, vk_timings* t, StageClock& clock) {
+    // v8 / v9 (f16 tables): the wave-list scan over the balanced partition with its final merge, one launch. The
+    // plan fixes the kernel instance, the partition and the scratch the launch needs (partial lists and per-slab
+    // counters); the launch takes that scratch from the caller.
+    struct WavePlan {
+        vk::WaveScanKernel kern;
+        size_t smem = 0;
+        int q = 1, ilp = 1, K = 0, per_cu = 1, lists_per_block = 1;
+        vk::plan::Partition part;
+        size_t part_pairs = 0;  // partial-list pairs: [slabs][q][max_slots][lists_per_block][K]
+    };
+
+    WavePlan plan_wave(size_t b, size_t kk, bool f16) const {
+        WavePlan w;
         // The wave lists take any length up to 128, so they hold exactly k entries: every one of k..K-1 that a
         // rounded-up K would keep costs inserts (about K * ln(n / K) per list) and buys nothing.
-        const int K = static_cast<int>(kk);
-        const int segments = K <= vk::WAVE ? 1 : 2;
+        w.K = static_cast<int>(kk);
+        const int segments = w.K <= vk::WAVE ? 1 : 2;
         const size_t entry_bytes = f16 ? 2 : sizeof(float);
-        const int q = vk::plan::cap_q_by_batch(
-            vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, false, K, entry_bytes), b);
+        w.q = vk::plan::cap_q_by_batch(
+            vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, false, w.K, entry_bytes), b);
         // fp32: 8 queries are two groups of 4 (16-byte reads); fp16: up to 8 queries in one group.
-        const int qg = (!f16 && q == 8) ? 4 : q, ng = (!f16 && q == 8) ? 2 : 1;
-        const int ilp = tuning.vectors_per_step;
-        vk::WaveScanKernel kern = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments, f16);
-        if (!kern.fn) fail(VK_ERR_LOGIC, "no fused-warp kernel built for this (Q, ILP, m, K)");
-        const size_t tables = static_cast<size_t>(q) * m * vk::KSUB * entry_bytes;
+        const int qg = (!f16 && w.q == 8) ? 4 : w.q, ng = (!f16 && w.q == 8) ? 2 : 1;
+        w.ilp = tuning.vectors_per_step;
+        w.kern = vk::fused_wave_kernel(qg, ng, w.ilp, static_cast<int>(m), segments, f16);
+        if (!w.kern.fn) fail(VK_ERR_LOGIC, "no fused-warp kernel built for this (Q, ILP, m, K)");
+        const size_t tables = static_cast<size_t>(w.q) * m * vk::KSUB * entry_bytes;
         require(tables <= info.max_smem_per_block, "LUT does not fit in LDS");
-        const size_t smem = kern.dynamic_lds ? tables : 0;  // fixed-m instances hold the tables in static LDS
-        if (kern.dynamic_lds)
-            VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-        int per_cu = 0;
-        VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
-        per_cu = std::max(per_cu, 1);
+        w.smem = w.kern.dynamic_lds ? tables : 0;  // fixed-m instances hold the tables in static LDS
+        if (w.kern.dynamic_lds)
+            VK_HIP(hipFuncSetAttribute(w.kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(w.smem)));
+        VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&w.per_cu, w.kern.fn, w.kern.threads, w.smem));
+        w.per_cu = std::max(w.per_cu, 1);
 
-        const vk::plan::Partition part_plan = vk::plan::balanced_partition(
-            static_cast<int64_t>(n), b, q, ilp, static_cast<int64_t>(per_cu) * info.sm_count, tuning.blocks_per_query,
-            info.sm_count);
+        w.part = vk::plan::balanced_partition(static_cast<int64_t>(n), b, w.q, w.ilp,
+                                              static_cast<int64_t>(w.per_cu) * info.sm_count,
+                                              tuning.blocks_per_query, info.sm_count);
         // Few vectors per block: the instance that admits candidates in bulk, if it has the same residency (the
         // partition above was planned with it).
-        if (!f16 && segments == 1 && q > 1 && vk::plan::bulk_scan(part_plan, ilp)) {
-            const vk::WaveScanKernel bulk = vk::fused_wave_kernel(qg, ng, ilp, static_cast<int>(m), segments, f16, true);
+        if (!f16 && segments == 1 && w.q > 1 && vk::plan::bulk_scan(w.part, w.ilp)) {
+            const vk::WaveScanKernel bulk = vk::fused_wave_kernel(qg, ng, w.ilp, static_cast<int>(m), segments, f16,
+                                                                  true);
             int bulk_per_cu = 0;
             if (bulk.fn) {
                 if (bulk.dynamic_lds)
                     VK_HIP(hipFuncSetAttribute(bulk.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(smem)));
-                VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&bulk_per_cu, bulk.fn, bulk.threads, smem));
+                                               static_cast<int>(w.smem)));
+                VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&bulk_per_cu, bulk.fn, bulk.threads, w.smem));
             }
-            if (bulk.fn && std::max(bulk_per_cu, 1) == per_cu) kern = bulk;
+            if (bulk.fn && std::max(bulk_per_cu, 1) == w.per_cu) w.kern = bulk;
         }
         // Up to 8 blocks per slab every wave leaves its own partial lists; beyond that the block merges its wave
         // lists first, which keeps the final merge of a slab to at most max(64, blocks per slab) lists per query.
-        const int lists_per_block = part_plan.max_slots > 8 ? 1 : kern.threads / vk::WAVE;
-        part.ensure(static_cast<size_t>(part_plan.slabs) * q * part_plan.max_slots * lists_per_block * K);
-        ensure_counters(static_cast<size_t>(part_plan.slabs));
+        w.lists_per_block = w.part.max_slots > 8 ? 1 : w.kern.threads / vk::WAVE;
+        w.part_pairs = static_cast<size_t>(w.part.slabs) * w.q * w.part.max_slots * w.lists_per_block * w.K;
+        return w;
+    }
 
+    // One launch of a planned wave-list scan over this batch's b device queries d_q into d_out (b x kk). part and
+    // counters: scratch of w.part_pairs pairs and w.part.slabs zeroed counters (the kernel leaves them at zero).
+    void launch_wave(const WavePlan& w, const float* d_q, size_t b, size_t kk, Pair* d_out, Pair* part_buf,
+                     unsigned* counter_buf) {
         last = vk_launch_shape{};
-        last.threads = kern.threads;
-        last.blocks_x = static_cast<int>(part_plan.grid);
+        last.threads = w.kern.threads;
+        last.blocks_x = static_cast<int>(w.part.grid);
         last.grid_y = 1;
-        last.queries_per_block = q;
-        last.vectors_per_step = ilp;
-        last.blocks_per_sm = per_cu;
-        last.waves = static_cast<double>(part_plan.grid) / (static_cast<double>(per_cu) * info.sm_count);
+        last.queries_per_block = w.q;
+        last.vectors_per_step = w.ilp;
+        last.blocks_per_sm = w.per_cu;
+        last.waves = static_cast<double>(w.part.grid) / (static_cast<double>(w.per_cu) * info.sm_count);
 
         // One launch: every block builds its slab's tables in LDS, scans, and the last block of each slab merges
-        // the slab's partial lists into d_out. The LUT and the final merge are inside scan_ms.
+        // the slab's partial lists into d_out.
         vk::WaveScanArgs a{};
         a.queries = d_q;
         a.centroids = centroids.get();
@@ -328,17 +344,26 @@ struct vk_searcher {
         a.d = static_cast<int>(d);
         a.m = static_cast<int>(m);
         a.nq = static_cast<int>(b);
-        a.K = K;
+        a.K = w.K;
         a.k = static_cast<int>(kk);
-        a.n_gran = part_plan.n_gran;
-        a.total = part_plan.total;
-        a.max_slots = part_plan.max_slots;
-        a.lists_per_block = lists_per_block;
-        a.part = part.get();
-        a.counters = counters.get();
+        a.n_gran = w.part.n_gran;
+        a.total = w.part.total;
+        a.max_slots = w.part.max_slots;
+        a.lists_per_block = w.lists_per_block;
+        a.part = part_buf;
+        a.counters = counter_buf;
         a.out = d_out;
+        VK_HIP(w.kern.launch(a, static_cast<int>(w.part.grid), w.smem, stream));
+    }
+
+    // d_q: device queries of this batch; writes b x kk results to d_out, with the searcher's own scratch buffers.
+    // The LUT and the final merge are inside scan_ms.
+    void run_wave(const float* d_q, size_t b, size_t kk, bool f16, Pair* d_out, vk_timings* t, StageClock& clock) {
+        const WavePlan w = plan_wave(b, kk, f16);
+        part.ensure(w.part_pairs);
+        ensure_counters(static_cast<size_t>(w.part.slabs));
         counters_dirty = true;  // cleared once the stream completes the launch without error
-        clock.time(&t->scan_ms, [&] { VK_HIP(kern.launch(a, static_cast<int>(part_plan.grid), smem, stream)); });
+        clock.time(&t->scan_ms, [&] { launch_wave(w, d_q, b, kk, d_out, part.get(), counters.get()); });
     }
 
     // Per-slab completion counters of the wave-list scan. The kernel leaves them at zero; they are zeroed here
@@ -383,12 +408,52 @@ struct vk_searcher {
         clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
     }
 
-    // v4-v7: per-thread-list fused scans on a (blocks_x, query groups) grid, then the final merge.
+    // v4: per-thread lists in LDS on a (blocks_x, nq) grid (searcher.cu:299-312: blocks_x from the fill rule with
+    // 256 threads, at most ceil(n / threads)), then the final merge of the blocks_x partial lists per query. The
+    // block size is the largest of 256, 128, 64 whose table, lists and merge buffer fit in LDS.
+    void run_list(const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
+        const int K = vk::plan::dispatched_k(kk);
+        int threads = 0;
+        for (int cand : {256, 128, 64})
+            if (vk::fused_list_lds(static_cast<int>(m), K, cand) <= info.max_smem_per_block) {
+                threads = cand;
+                break;
+            }
+        if (threads == 0)
+            fail(VK_ERR_RUNTIME, "v4_fused: the LUT and one wave's per-thread lists (" +
+                                     std::to_string(vk::fused_list_lds(static_cast<int>(m), K, 64)) +
+                                     " B) do not fit in LDS; use v5_fused_reg or later");
+        const vk::ThreadScanKernel kern = vk::fused_list_kernel(K, threads);
+        if (!kern.fn) fail(VK_ERR_LOGIC, "no v4 kernel built for this K");
+        const size_t smem = vk::fused_list_lds(static_cast<int>(m), K, threads);
+        VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+        int64_t bx = vk::plan::blocks_x_fill(static_cast<int64_t>(n), static_cast<int64_t>(b), 256, info.sm_count,
+                                             tuning.blocks_per_query);
+        bx = std::max<int64_t>(1, std::min<int64_t>(bx, (static_cast<int64_t>(n) + threads - 1) / threads));
+        last = vk_launch_shape{threads, static_cast<int>(bx), static_cast<int>(b), 1, 1, 0, 0.0};
+        lut.ensure(b * m * vk::KSUB);
+        part.ensure(b * static_cast<size_t>(bx) * K);
+        clock.time(&t->lut_ms, [&] {
+            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(b), 1,
+                                  static_cast<int>(b), lut.get(), stream));
+        });
+        vk::ThreadScanArgs a{lut.get(), codes_il.get(), codes_v.get(), static_cast<int64_t>(n), static_cast<int>(m),
+                             static_cast<int>(b), part.get()};
+        clock.time(&t->scan_ms, [&] {
+            VK_HIP(kern.launch(a, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(b)), smem, stream));
+        });
+        vk::SelectArgs s{};
+        s.mode = 1;
+        s.part = part.get();
+        s.K = K;
+        s.bx = bx;
+        s.k = static_cast<int>(kk);
+        s.out = d_out;
+        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
+    }
+
+    // v5-v7: per-thread-list fused scans on a (blocks_x, query groups) grid, then the final merge.
     void run_thread(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
-        if (v == VK_V4_FUSED)
-            fail(VK_ERR_LOGIC,
-                 "v4_fused is not launched in this build: its run-time-indexed per-thread list faulted the GPU "
-                 "(memory-aperture violation, cause not yet established); use v5_fused_reg or later");
         const int K = vk::plan::dispatched_k(kk);
         const int q = v == VK_V7_FUSED_VEC_MQ
                           ? vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, true, K)
@@ -402,21 +467,15 @@ struct vk_searcher {
         require(smem <= info.max_smem_per_block, "LUT does not fit in LDS");
         VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
         const int64_t grid_y = (static_cast<int64_t>(b) + q - 1) / q;
-        int64_t bx = 1;
         last = vk_launch_shape{};
-        if (v == VK_V4_FUSED) {
-            bx = vk::plan::blocks_x_fill(static_cast<int64_t>(n), static_cast<int64_t>(b), 256, info.sm_count,
-                                         tuning.blocks_per_query);
-        } else {
-            int per_cu = 0;
-            VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
-            const vk::plan::WaveChoice c = vk::plan::blocks_x_waves(
-                static_cast<int64_t>(n), grid_y, kern.threads, static_cast<int64_t>(std::max(per_cu, 1)) * info.sm_count,
-                tuning.blocks_per_query);
-            bx = c.blocks_x;
-            last.blocks_per_sm = per_cu;
-            last.waves = c.waves;
-        }
+        int per_cu = 0;
+        VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern.fn, kern.threads, smem));
+        const vk::plan::WaveChoice c = vk::plan::blocks_x_waves(
+            static_cast<int64_t>(n), grid_y, kern.threads, static_cast<int64_t>(std::max(per_cu, 1)) * info.sm_count,
+            tuning.blocks_per_query);
+        int64_t bx = c.blocks_x;
+        last.blocks_per_sm = per_cu;
+        last.waves = c.waves;
         bx = std::max<int64_t>(1, std::min<int64_t>(bx, (static_cast<int64_t>(n) + kern.threads - 1) / kern.threads));
         last.threads = kern.threads;
         last.blocks_x = static_cast<int>(bx);
@@ -449,16 +508,13 @@ struct vk_searcher {
     void run_variant(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
         if (v == VK_V8_FUSED_WARP || v == VK_V9_FUSED_WARP_F16)
             return run_wave(d_q, b, kk, v == VK_V9_FUSED_WARP_F16, d_out, t, clock);
+        if (v == VK_V4_FUSED) return run_list(d_q, b, kk, d_out, t, clock);
         if (vk_is_fused(v)) return run_thread(v, d_q, b, kk, d_out, t, clock);
         run_unfused(v, d_q, b, kk, d_out, t, clock);
     }
 
     void check_search(size_t kk, int v) const {
         require(valid_variant(v), "unknown scan variant " + std::to_string(v));
-        if (v == VK_V4_FUSED)
-            fail(VK_ERR_LOGIC,
-                 "v4_fused is not launched in this build: its run-time-indexed per-thread list faulted the GPU "
-                 "(memory-aperture violation, cause not yet established); use v5_fused_reg or later");
         require(kk >= 1 && kk <= 128 && kk <= n, "k must be in [1, min(128, n)]");
         validate(v);
     }
