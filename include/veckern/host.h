@@ -1,8 +1,8 @@
 /*
  * host.h — C API of libveckern_cpu.so, the host-side tools around the GPU search: seeded synthetic data, the
- * PQ codec (k-means training, encoding) and recall evaluation. They build the search path's inputs and score
- * its outputs (the C++ interfaces are veckern/io.hpp, veckern/pq.hpp and veckern/eval.hpp); the search itself
- * is veckern.h. Status codes: 0 on success, 2 on error with vkh_last_error() set.
+ * PQ codec (k-means training, encoding), recall evaluation and the CPU search path. They build the search
+ * path's inputs, score its outputs and time the CPU beside the GPU (the C++ interfaces are veckern/io.hpp,
+ * veckern/pq.hpp, veckern/eval.hpp and veckern/cpu_ref.hpp); the GPU search is veckern.h. Status codes: 0 on success, 2 on error with vkh_last_error() set.
  */
 #ifndef VECKERN_HOST_H
 #define VECKERN_HOST_H
@@ -40,6 +40,14 @@ int vkh_pq_train(const float* x, size_t n, size_t d, size_t m, size_t iters, uin
 /* Nearest-centroid codes for x (n x d) under the given codebook. codes: n x m. */
 int vkh_pq_encode(const float* centroids, size_t d, size_t m, const float* x, size_t n, uint8_t* codes);
 int vkh_pq_decode(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n, float* x);
+
+/* The CPU search path (veckern/cpu_ref.hpp) under the given [m][256][d/m] codebook: compute_lut (lut: nq x m x 256),
+ * adc_scan (dists: nq x n), select_topk (rows of n distances, out: nq x k), adc_search (out: nq x k). */
+int vkh_compute_lut(const float* centroids, size_t d, size_t m, const float* queries, size_t nq, float* lut);
+int vkh_adc_scan(const float* lut, size_t nq, const uint8_t* codes, size_t n, size_t m, float* dists);
+int vkh_select_topk(const float* dists, size_t nq, size_t n, size_t k, vk_neighbor* out);
+int vkh_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n, const float* queries,
+                   size_t nq, size_t k, vk_neighbor* out);
 
 /* veckern::exact_knn / rerank_exact / recall_at_k. recall returns -1 on error. */
 int vkh_exact_knn(const float* base, size_t n, const float* queries, size_t nq, size_t d, size_t k,

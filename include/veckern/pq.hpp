@@ -20,9 +20,10 @@ public:
     // Throws std::runtime_error unless d is a positive multiple of m.
     ProductQuantizer(std::size_t d, std::size_t m);
 
-    // Independent k-means per sub-space on the first n rows of x (row-major n x d): 256 distinct training
-    // points as the initial centroids, then `iters` rounds of nearest-centroid assignment and mean update;
-    // an empty cluster is re-seeded with a random training point. Deterministic for a given seed.
+    // Independent k-means per sub-space on the first n rows of x (row-major n x d), the reference's algorithm and
+    // random stream (pq.cpp:31-69): initial centroids are 256 distinct points picked by a std::shuffle driven by
+    // std::mt19937_64(seed), then `iters` rounds of nearest-centroid assignment and float mean update; an empty
+    // cluster restarts at a random point. The same arguments give the reference's codebook bit for bit.
     void train(const float* x, std::size_t n, std::size_t iters = 20, uint64_t seed = 1);
     // The same training with the assignment step delegated (the update, initialisation and re-seeding stay here).
     void train(const float* x, std::size_t n, std::size_t iters, uint64_t seed, AssignFn assign, void* context);

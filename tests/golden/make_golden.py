@@ -13,6 +13,10 @@ Fixtures:
   tiny_diffs.npz     centroids within 1e-20 of the query: squared differences underflow to subnormals / zero
   topk_kat.npz       the reference's TopK known-answer case and padding (tests/test_cpu.cpp:33-46)
   recall_kat.npz     recall_at_k on hand-made rows with padding ids and repeated ids
+  train_kmeans.npz   ProductQuantizer::train codebooks: clustered data; rows repeated so that most clusters go
+                     empty and are re-seeded; zero iterations (the shuffled initial points alone)
+
+`python make_golden.py NAME ...` writes only the named fixtures.
 """
 import os
 import sys
@@ -75,10 +79,31 @@ def save(name, **arrays):
     print(f"wrote {path} ({os.path.getsize(path) / 1024:.1f} KiB)")
 
 
+def write_train_fixture():
+    rng = np.random.default_rng(17)
+    cases = []
+    cases.append((ref_clustered(700, 16, 10, 3), 4, 3, 5))
+    distinct = rng.standard_normal((40, 8)).astype(np.float32)
+    cases.append((distinct[rng.integers(0, 40, size=300)], 2, 2, 9))  # 40 distinct rows: >= 216 empty clusters
+    cases.append((ref_clustered(400, 32, 7, 4), 8, 0, 1))
+    arrays = {}
+    for j, (x, m, iters, seed) in enumerate(cases):
+        cent, _ = ref_train(x, m, iters, seed)
+        arrays.update({f"x{j}": x, f"m{j}": np.int64(m), f"iters{j}": np.int64(iters), f"seed{j}": np.int64(seed),
+                       f"centroids{j}": cent})
+    save("train_kmeans.npz", cases=np.int64(len(cases)), **arrays)
+
+
 def main():
     if not b.ref_available():
         sys.exit("oracle/_ref/libvkref.so is not built (make -C oracle ref, with the reference checkout present)")
+    only = set(sys.argv[1:])
+    if only:
+        if "train_kmeans.npz" in only:
+            write_train_fixture()
+        return
 
+    write_train_fixture()
     for m, n, d, nq, ks, name in [(8, 2000, 32, 5, (1, 10, 100), "clustered_m8.npz"),
                                   (16, 2003, 64, 5, (10, 33, 128), "clustered_m16.npz")]:
         base = ref_clustered(n, d, 20, 7)

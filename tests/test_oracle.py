@@ -73,8 +73,9 @@ def test_recall_known_answer():
 
 
 def test_every_golden_file_is_checked():
+    # train_kmeans.npz pins the product's PQ trainer (tests/test_cpu_path.py); the oracle has no trainer
     names = {os.path.basename(p) for p in glob.glob(os.path.join(GOLDEN, "*.npz"))}
-    assert names == set(FIXTURES) | {"topk_kat.npz", "recall_kat.npz"}
+    assert names == set(FIXTURES) | {"topk_kat.npz", "recall_kat.npz", "train_kmeans.npz"}
 
 
 # ---------------------------------------------------------------- 2. the reference's compiled CPU code, live

@@ -11,6 +11,7 @@
 #endif
 
 #include "philox.hpp"
+#include "veckern/cpu_ref.hpp"
 #include "veckern/eval.hpp"
 #include "veckern/io.hpp"
 #include "veckern/pq.hpp"
@@ -100,6 +101,27 @@ VKH_EXPORT int vkh_pq_encode(const float* centroids, size_t d, size_t m, const f
 
 VKH_EXPORT int vkh_pq_decode(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n, float* x) {
     return guarded([&] { make_pq(centroids, d, m).decode(codes, n, x); });
+}
+
+VKH_EXPORT int vkh_compute_lut(const float* centroids, size_t d, size_t m, const float* queries, size_t nq,
+                               float* lut) {
+    return guarded([&] { veckern::compute_lut(make_pq(centroids, d, m), queries, nq, lut); });
+}
+
+VKH_EXPORT int vkh_adc_scan(const float* lut, size_t nq, const uint8_t* codes, size_t n, size_t m, float* dists) {
+    return guarded([&] { veckern::adc_scan(lut, nq, codes, n, m, dists); });
+}
+
+VKH_EXPORT int vkh_select_topk(const float* dists, size_t nq, size_t n, size_t k, vk_neighbor* out) {
+    return guarded([&] { veckern::select_topk(dists, nq, n, k, reinterpret_cast<veckern::Neighbor*>(out)); });
+}
+
+VKH_EXPORT int vkh_adc_search(const float* centroids, size_t d, size_t m, const uint8_t* codes, size_t n,
+                              const float* queries, size_t nq, size_t k, vk_neighbor* out) {
+    return guarded([&] {
+        veckern::adc_search(make_pq(centroids, d, m), codes, n, queries, nq, k,
+                            reinterpret_cast<veckern::Neighbor*>(out));
+    });
 }
 
 VKH_EXPORT int vkh_exact_knn(const float* base, size_t n, const float* queries, size_t nq, size_t d, size_t k,

@@ -93,8 +93,6 @@ enum Stream : uint32_t {
     kBlobCentres = 10,
     kBlobCluster = 11,
     kBlobNoise = 12,
-    kTrainInit = 20,
-    kTrainReseed = 21,
 };
 
 }  // namespace veckern::rng

@@ -1,16 +1,19 @@
 // Product quantizer training and coding on the host (reference interface: include/veckern/pq.hpp,
-// src/cpu/pq.cpp). Same algorithm family as the reference — per sub-space k-means from 256 distinct training
-// points, empty clusters re-seeded from a random point, nearest centroid with the lowest index on ties — with
-// this library's own seeded generator, so codebooks differ from the reference's for the same seed.
+// src/cpu/pq.cpp). Training reproduces the reference's k-means exactly (pq.cpp:31-69), so the same (x, n, iters,
+// seed) gives the reference's codebook byte for byte: one std::mt19937_64 seeded once and consumed in the
+// reference's order (a std::shuffle of the point indices per sub-space, then one draw per empty cluster), float
+// sums in point order, and the first minimum of l2sq as the assignment. The assignment step is pluggable
+// (gpu::train passes the GPU kernel, which returns the same indices).
 //
-// Nearest-centroid search keeps a transposed codebook [dsub][256] per sub-space so that the 256 distances of
-// one sub-vector are computed in a loop over centroids the compiler vectorises.
+// Nearest-centroid search on the host keeps a transposed codebook [dsub][256] per sub-space so that the 256
+// distances of one sub-vector are computed in a loop over centroids the compiler vectorises; each distance is
+// still summed over j in order, the arithmetic of l2sq.
 #include <algorithm>
 #include <limits>
 #include <numeric>
+#include <random>
 #include <vector>
 
-#include "philox.hpp"
 #include "veckern/pq.hpp"
 
 namespace veckern {
@@ -76,40 +79,41 @@ void ProductQuantizer::train(const float* x, std::size_t n, std::size_t iters, u
                              void* context) {
     check(n >= kSubCentroids, "PQ training needs at least 256 vectors");
     check(assign_fn != nullptr, "assignment function is null");
-    std::vector<float> sub(n * dsub_);
+    std::mt19937_64 rng(seed);  // one stream for the whole codebook, sub-space after sub-space
+    std::vector<float> sub(n * dsub_), sums(kSubCentroids * dsub_);
     std::vector<uint32_t> assign(n);
     std::vector<std::size_t> counts(kSubCentroids), order(n);
-    std::vector<double> sums(kSubCentroids * dsub_);
-    uint64_t reseeds = 0;
 
     for (std::size_t s = 0; s < m_; ++s) {
         for (std::size_t i = 0; i < n; ++i) std::copy_n(x + i * d_ + s * dsub_, dsub_, sub.data() + i * dsub_);
         float* cent = centroids_.data() + s * kSubCentroids * dsub_;
 
-        // 256 distinct training points: the first 256 positions of a seeded Fisher-Yates shuffle.
-        std::iota(order.begin(), order.end(), 0);
-        for (std::size_t c = 0; c < kSubCentroids; ++c) {
-            const uint64_t r = rng::bits64(seed, rng::kTrainInit, s * kSubCentroids + c);
-            std::swap(order[c], order[c + r % (n - c)]);
+        // Initial centroids: the points at the first 256 positions of a shuffled index order (distinct points).
+        std::iota(order.begin(), order.end(), std::size_t{0});
+        std::shuffle(order.begin(), order.end(), rng);
+        for (std::size_t c = 0; c < kSubCentroids; ++c)
             std::copy_n(sub.data() + order[c] * dsub_, dsub_, cent + c * dsub_);
-        }
 
         for (std::size_t it = 0; it < iters; ++it) {
             assign_fn(sub.data(), n, cent, dsub_, assign.data(), context);
-            std::fill(sums.begin(), sums.end(), 0.0);
-            std::fill(counts.begin(), counts.end(), 0);
+            // Mean update: float sums accumulated in point order, then one division per coordinate.
+            std::fill(sums.begin(), sums.end(), 0.f);
+            std::fill(counts.begin(), counts.end(), std::size_t{0});
             for (std::size_t i = 0; i < n; ++i) {
-                ++counts[assign[i]];
-                for (std::size_t j = 0; j < dsub_; ++j) sums[assign[i] * dsub_ + j] += sub[i * dsub_ + j];
+                const std::size_t c = assign[i];
+                ++counts[c];
+                const float* p = sub.data() + i * dsub_;
+                float* acc = sums.data() + c * dsub_;
+                for (std::size_t j = 0; j < dsub_; ++j) acc[j] += p[j];
             }
             for (std::size_t c = 0; c < kSubCentroids; ++c) {
-                if (counts[c] == 0) {  // re-seed an empty cluster with a random training point
-                    const uint64_t r = rng::bits64(seed, rng::kTrainReseed, reseeds++);
-                    std::copy_n(sub.data() + (r % n) * dsub_, dsub_, cent + c * dsub_);
+                float* dst = cent + c * dsub_;
+                if (counts[c] == 0) {  // an empty cluster restarts at a random point (one draw, in cluster order)
+                    std::copy_n(sub.data() + (rng() % n) * dsub_, dsub_, dst);
                     continue;
                 }
-                for (std::size_t j = 0; j < dsub_; ++j)
-                    cent[c * dsub_ + j] = static_cast<float>(sums[c * dsub_ + j] / static_cast<double>(counts[c]));
+                const float count = static_cast<float>(counts[c]);
+                for (std::size_t j = 0; j < dsub_; ++j) dst[j] = sums[c * dsub_ + j] / count;
             }
         }
     }

@@ -1,5 +1,6 @@
 """Host-side tools of veckern_amd (lib/libveckern_cpu.so, include/veckern/host.h): seeded synthetic data, the PQ
-codec and recall evaluation. They build the GPU search's inputs and score its outputs; they are not a search path.
+codec, recall evaluation, and the CPU search path (veckern/cpu_ref.hpp) that the benchmark driver times beside the
+GPU. They build the GPU search's inputs, score its outputs and give its CPU counterpart.
 """
 from __future__ import annotations
 
@@ -38,6 +39,10 @@ def library() -> ctypes.CDLL:
         lib.vkh_pq_train.argtypes = [_P, _S, _S, _S, _S, ctypes.c_uint64, _P]
         lib.vkh_pq_encode.argtypes = [_P, _S, _S, _P, _S, _P]
         lib.vkh_pq_decode.argtypes = [_P, _S, _S, _P, _S, _P]
+        lib.vkh_compute_lut.argtypes = [_P, _S, _S, _P, _S, _P]
+        lib.vkh_adc_scan.argtypes = [_P, _S, _P, _S, _S, _P]
+        lib.vkh_select_topk.argtypes = [_P, _S, _S, _S, _P]
+        lib.vkh_adc_search.argtypes = [_P, _S, _S, _P, _S, _P, _S, _S, _P]
         lib.vkh_exact_knn.argtypes = [_P, _S, _P, _S, _S, _S, _P]
         lib.vkh_rerank_exact.argtypes = [_P, _S, _P, _S, _P, _S, _S, _P]
         lib.vkh_recall_at_k.restype = ctypes.c_double
@@ -118,6 +123,49 @@ def pq_decode(centroids: np.ndarray, codes: np.ndarray, d: int) -> np.ndarray:
     x = np.empty((n, d), dtype=np.float32)
     _check(library().vkh_pq_decode(cent.ctypes.data, d, m, codes.ctypes.data, n, x.ctypes.data))
     return x
+
+
+def compute_lut(centroids: np.ndarray, queries: np.ndarray) -> np.ndarray:
+    """The CPU path's tables: (nq, m, 256) squared sub-distances."""
+    cent = np.ascontiguousarray(centroids, dtype=np.float32)
+    m = cent.shape[0]
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    nq, d = q.shape
+    lut = np.empty((nq, m, 256), dtype=np.float32)
+    _check(library().vkh_compute_lut(cent.ctypes.data, d, m, q.ctypes.data, nq, lut.ctypes.data))
+    return lut
+
+
+def adc_scan(lut: np.ndarray, codes: np.ndarray) -> np.ndarray:
+    """The CPU path's ADC distances: (nq, n)."""
+    lut = np.ascontiguousarray(lut, dtype=np.float32)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    n, m = codes.shape
+    nq = lut.size // (m * 256)
+    out = np.empty((nq, n), dtype=np.float32)
+    _check(library().vkh_adc_scan(lut.ctypes.data, nq, codes.ctypes.data, n, m, out.ctypes.data))
+    return out
+
+
+def select_topk(dists: np.ndarray, k: int) -> np.ndarray:
+    dists = np.ascontiguousarray(dists, dtype=np.float32)
+    nq, n = dists.shape
+    out = np.empty((nq, k), dtype=NEIGHBOR_DTYPE)
+    _check(library().vkh_select_topk(dists.ctypes.data, nq, n, k, out.ctypes.data))
+    return out
+
+
+def adc_search(centroids: np.ndarray, codes: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
+    """The CPU search path (LUT, scan and top-k per query on all host threads): (nq, k) neighbours."""
+    cent = np.ascontiguousarray(centroids, dtype=np.float32)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    n, m = codes.shape
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    nq, d = q.shape
+    out = np.empty((nq, k), dtype=NEIGHBOR_DTYPE)
+    _check(library().vkh_adc_search(cent.ctypes.data, d, m, codes.ctypes.data, n, q.ctypes.data, nq, k,
+                                    out.ctypes.data))
+    return out
 
 
 def exact_knn(base: np.ndarray, queries: np.ndarray, k: int) -> np.ndarray:
