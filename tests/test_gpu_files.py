@@ -58,6 +58,8 @@ def test_fvecs_inputs_with_ivecs_ground_truth(tmp_path):
         assert int(rows["v8_fused_warp"]["n"]) == N and int(rows["v8_fused_warp"]["d"]) == D
         assert float(rows["v8_fused_warp"]["recall"]) == pytest.approx(fp32, abs=1e-6)
         assert float(rows["v9_fused_warp_f16"]["recall"]) == pytest.approx(fp16, abs=1e-6)
+        # the CPU search path's row (all NQ queries, the default --cpu-queries 100 capped at nq) scores the same
+        assert float(rows["cpu_reference"]["recall"]) == pytest.approx(fp32, abs=1e-6)
 
 
 def test_bvecs_inputs(tmp_path):
