@@ -62,7 +62,7 @@ CASE("blocks_x_fill: ~8 blocks per CU over the grid, >= 16 vectors per thread, o
 }
 
 CASE("bulk admission is chosen while a block scans few vectors of a slab") {
-    // 100k vectors, nq=100, Q=4: 9 blocks per slab, ~11k vectors each
+    // 100k vectors, nq=100, Q=4: 13 blocks per slab, ~7.7k vectors each
     EXPECT(bulk_scan(balanced_partition(100'000, 100, 4, 4, 512, 0, 256), 4));
     // 10M vectors, nq=8, Q=4: 2 slabs of 256 blocks, ~39k vectors each
     EXPECT(bulk_scan(balanced_partition(10'000'000, 8, 4, 4, 512, 0, 256), 4));
@@ -89,8 +89,10 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
     EXPECT(b.grid == 500 && b.max_slots == 2);
     EXPECT(balanced_partition(1'000'000, 1000, 4, 4, 256, 0, 256).grid == 250);  // one block per slab
     EXPECT(balanced_partition(1'000'000, 1000, 2, 4, 256, 0, 256).grid == 256);  // 500 slabs > 256 slots
-    // small slabs: at least kMinBlockVectors vectors per block (100k vectors = 391 granules of 256: 9 blocks each)
-    EXPECT(balanced_partition(100'000, 100, 4, 4, 512, 0, 256).grid == 25 * 9);
+    // small slabs: at most ceil(n / kMinBlockVectors) blocks each (100k vectors: 13 blocks of ~7.7k vectors)
+    EXPECT(balanced_partition(100'000, 100, 4, 4, 512, 0, 256).grid == 25 * 13);
+    // one query: spread over ceil(n / (16 x 512)) blocks when the CUs allow (the reference's rule)
+    EXPECT(balanced_partition(50'003, 1, 1, 4, 512, 0, 256).grid == 7);
     EXPECT(balanced_partition(1'000, 1, 1, 4, 512, 0, 256).grid == 1);
     std::mt19937_64 rng(7);
     for (int trial = 0; trial < 300; ++trial) {

@@ -95,9 +95,8 @@ def test_single_query_spreads_over_the_device(fixture, searcher):
     d, i, _ = searcher.search(queries[:1], 10, vk.ScanVariant.FusedWarp)
     assert_same(d, i, expected(fixture, 10)[:1], "v8 nq=1")
     s = searcher.last_launch()
-    # spread over the device: a block per ~10k vectors (40 granules of 256), at most one per CU
-    granules = np.ceil(N / 256.0)
-    expected_blocks = min(vk.device_info().sm_count, max(1, int(granules // 40)))
+    # spread over ceil(n / (16 vectors x 512 threads)) blocks (the reference's rule), at most one per CU
+    expected_blocks = min(vk.device_info().sm_count, -(-N // 8192))
     assert s.blocks_x == expected_blocks and s.blocks_x > 1
 
 
@@ -125,7 +124,7 @@ def test_long_lists_merge_whole(family):
 def test_bulk_and_one_by_one_admission_agree():
     # Blocks that scan few vectors of a slab use the instance admitting candidates in bulk; above 2^18 vectors per
     # block and slab the one admitting them one by one (the headline's). 300k vectors with one block per slab take
-    # the second, the default spread (~10k vectors per block) the first; both must equal the oracle.
+    # the second, the default spread (~8k vectors per block) the first; both must equal the oracle.
     n, d, m, nq = 300_007, 64, 16, 9
     centroids, codes, queries = datagen.random_fixture(n, d, m, nq, seed=41)
     with vk.PQSearcher(centroids, codes, d) as s:

@@ -42,12 +42,16 @@ inline int64_t first_block(int64_t item, int64_t grid, int64_t total) { return (
 // Balanced partition of the wave-list scan: slabs of q queries, each cut into granules of 64*ilp vectors;
 // the slabs*n_gran items are split evenly over `grid` blocks. blocks_per_query > 0 fixes the blocks per slab.
 // Otherwise, when the slabs are no more than the resident blocks (`slots`), each slab gets floor(slots / slabs)
-// blocks, at most `cus` (> 0) of them and each with at least kMinBlockVectors vectors, so that no block crosses a
+// blocks, at most `cus` (> 0) of them and at most ceil(n / kMinBlockVectors), so that no block crosses a
 // slab boundary; with more slabs than slots, grid = slots and blocks span slab boundaries. Measured on MI355X: with a block per resident slot and ranges
 // crossing slabs, the two blocks sharing a CU finish ~0.4 ms apart at 1M x nq=1000 (the older block's waves get
 // issue priority) and the search takes 1.43 ms; slab-aligned blocks take 1.35 ms (fp16 tables at Q = 8: 1.07 ->
 // 0.90 ms). A slab's blocks beyond one per CU only lengthen its final merge (nq = 1 at 10M: 73 -> 67 us).
-constexpr int64_t kMinBlockVectors = 10240;
+// kMinBlockVectors: 16 vectors per thread of a 512-thread block, the reference's rule for how far a search is spread
+// (searcher.cu:196-197; its tests/test_gpu.cpp:139-145 expect a single query over at least ceil(n / (16 * threads))
+// blocks). Fewer vectors per block and a block's table build and merges outweigh its scan (100k vectors, nq=100:
+// 20 blocks per slab 94 us, 10 blocks 78 us).
+constexpr int64_t kMinBlockVectors = 8192;
 
 struct Partition {
     int64_t slabs = 0, n_gran = 0, total = 0, grid = 0;
@@ -66,10 +70,7 @@ inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_
     if (per_slab <= 0 && p.slabs <= slots) {
         per_slab = slots / p.slabs;
         if (cus > 0) per_slab = std::min(per_slab, cus);
-        // At least ~10k vectors per block: below that a block's table build and merges outweigh its scan
-        // (100k vectors, nq=100: 20 blocks per slab 94 us, 10 blocks 78 us).
-        const int64_t min_gran = (kMinBlockVectors + 64 * ilp - 1) / (64 * ilp);
-        per_slab = std::max<int64_t>(1, std::min(per_slab, p.n_gran / min_gran));
+        per_slab = std::max<int64_t>(1, std::min(per_slab, (n + kMinBlockVectors - 1) / kMinBlockVectors));
     }
     if (per_slab > 0)
         p.grid = p.slabs * std::min<int64_t>(per_slab, p.n_gran);
