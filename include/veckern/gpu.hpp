@@ -18,7 +18,7 @@ enum class ScanVariant {
     SharedLut,     // v1: LUT staged in LDS
     SharedLutVec,  // v2: + 16-byte row loads (m % 16 == 0)
     Interleaved,   // v3: + wave64-interleaved byte layout
-    Fused,         // v4: interleaved scan fused with a per-thread list (kept in LDS)
+    Fused,         // v4: interleaved scan fused with a per-thread list (rejected before launch in this build)
     FusedReg,      // v5: per-thread list in registers
     FusedVec,      // v6: v5 + 16-byte-word interleaved layout (m % 16 == 0)
     FusedVecMQ,    // v7: v6 + Q queries per block sharing every code load (m % 16 == 0)

@@ -12,8 +12,9 @@ pytestmark = pytest.mark.gpu
 
 N, D, M, NQ = 50_003, 64, 16, 37
 SCAN = [vk.ScanVariant.GlobalLut, vk.ScanVariant.SharedLut, vk.ScanVariant.SharedLutVec, vk.ScanVariant.Interleaved]
-FUSED = [vk.ScanVariant.Fused, vk.ScanVariant.FusedReg, vk.ScanVariant.FusedVec, vk.ScanVariant.FusedVecMQ,
-         vk.ScanVariant.FusedWarp]
+# v4 (Fused) is rejected before launch in this build: its run-time-indexed per-thread list faulted the GPU with a
+# memory-aperture violation whose cause is not established, so it is not run here (see test_v4_is_rejected).
+FUSED = [vk.ScanVariant.FusedReg, vk.ScanVariant.FusedVec, vk.ScanVariant.FusedVecMQ, vk.ScanVariant.FusedWarp]
 
 
 @pytest.fixture(scope="module")
@@ -110,8 +111,7 @@ def test_m8_codes_rejected_by_word_variants_and_accepted_by_v5():
             with pytest.raises(vk.VkError):
                 s.search(queries, 10, v)
         exp = orc.adc_search(centroids, D, codes, queries, 10)
-        for v in (vk.ScanVariant.GlobalLut, vk.ScanVariant.Interleaved, vk.ScanVariant.Fused,
-                  vk.ScanVariant.FusedReg):
+        for v in (vk.ScanVariant.GlobalLut, vk.ScanVariant.Interleaved, vk.ScanVariant.FusedReg):
             d, i, _ = s.search(queries, 10, v)
             assert (i == exp["id"]).all() and (d.view(np.uint32) == exp["dist"].view(np.uint32)).all()
 
@@ -125,38 +125,17 @@ def test_invalid_tuning_and_k_are_rejected(fx):
         s.search(queries[:1], 129, vk.ScanVariant.FusedReg)
 
 
-def v4_threads(m, K, lds):
-    """v4's block size: the largest of 256, 128, 64 whose table, lists and merge buffer fit in LDS."""
-    for t in (256, 128, 64):
-        if m * 256 * 4 + t * K * 8 + (t // 64 + 1) * K * 8 <= lds:
-            return t
-    return 0
+def test_v4_is_rejected_before_launch(fx):
+    _, _, queries, s = fx
+    with pytest.raises(vk.VkLogicError, match="v4_fused is not launched"):
+        s.search(queries[:1], 10, vk.ScanVariant.Fused)
 
 
-def test_v4_parity(fx):
-    # v4 keeps a sorted K-list per thread in LDS (K = dispatched k: 8 .. 128); every K and block size it picks
-    lds = vk.device_info().max_smem_per_block
-    for k in (1, 8, 10, 16, 32, 33, 64, 100, 128):
-        check(fx, k, vk.ScanVariant.Fused)
-        shape = fx[3].last_launch()
-        assert shape.grid_y == NQ and shape.queries_per_block == 1
-        assert shape.threads == v4_threads(M, vk.dispatched_k(k), lds)
-    for bpq in (1, 5):
-        check(fx, 10, vk.ScanVariant.Fused, vk.Tuning(blocks_per_query=bpq))
-        assert fx[3].last_launch().blocks_x == bpq
-
-
-def test_v4_rejects_lists_that_do_not_fit_in_lds():
-    # d = 128, m = 128: a 128 KB LUT leaves room for 128 threads' lists of 16 (k = 10) but not for one wave's lists
-    # of 128 (k = 100)
-    centroids, codes, queries = datagen.random_fixture(3_001, 128, 128, 3, seed=5)
-    with vk.PQSearcher(centroids, codes, 128) as s:
-        exp = orc.adc_search(centroids, 128, codes, queries, 10)
-        d, i, _ = s.search(queries, 10, vk.ScanVariant.Fused)
-        assert (i == exp["id"]).all() and (d.view(np.uint32) == exp["dist"].view(np.uint32)).all()
-        assert s.last_launch().threads == v4_threads(128, 16, vk.device_info().max_smem_per_block) == 128
-        with pytest.raises(vk.VkError, match="do not fit in LDS"):
-            s.search(queries, 100, vk.ScanVariant.Fused)
+@pytest.mark.skip(reason="v4_fused faulted the GPU (memory-aperture violation with its list in scratch, reached "
+                         "through generic pointers by a non-inlined insert); the cause is not established, so no v4 "
+                         "kernel is run")
+def test_v4_parity():
+    pass
 
 
 def test_tie_heavy_data_every_variant():

@@ -408,50 +408,6 @@ struct vk_searcher {
         clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
     }
 
-    // v4: per-thread lists in LDS on a (blocks_x, nq) grid (searcher.cu:299-312: blocks_x from the fill rule with
-    // 256 threads, at most ceil(n / threads)), then the final merge of the blocks_x partial lists per query. The
-    // block size is the largest of 256, 128, 64 whose table, lists and merge buffer fit in LDS.
-    void run_list(const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
-        const int K = vk::plan::dispatched_k(kk);
-        int threads = 0;
-        for (int cand : {256, 128, 64})
-            if (vk::fused_list_lds(static_cast<int>(m), K, cand) <= info.max_smem_per_block) {
-                threads = cand;
-                break;
-            }
-        if (threads == 0)
-            fail(VK_ERR_RUNTIME, "v4_fused: the LUT and one wave's per-thread lists (" +
-                                     std::to_string(vk::fused_list_lds(static_cast<int>(m), K, 64)) +
-                                     " B) do not fit in LDS; use v5_fused_reg or later");
-        const vk::ThreadScanKernel kern = vk::fused_list_kernel(K, threads);
-        if (!kern.fn) fail(VK_ERR_LOGIC, "no v4 kernel built for this K");
-        const size_t smem = vk::fused_list_lds(static_cast<int>(m), K, threads);
-        VK_HIP(hipFuncSetAttribute(kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-        int64_t bx = vk::plan::blocks_x_fill(static_cast<int64_t>(n), static_cast<int64_t>(b), 256, info.sm_count,
-                                             tuning.blocks_per_query);
-        bx = std::max<int64_t>(1, std::min<int64_t>(bx, (static_cast<int64_t>(n) + threads - 1) / threads));
-        last = vk_launch_shape{threads, static_cast<int>(bx), static_cast<int>(b), 1, 1, 0, 0.0};
-        lut.ensure(b * m * vk::KSUB);
-        part.ensure(b * static_cast<size_t>(bx) * K);
-        clock.time(&t->lut_ms, [&] {
-            VK_HIP(vk::launch_lut(d_q, centroids.get(), static_cast<int>(d), static_cast<int>(m), static_cast<int>(b), 1,
-                                  static_cast<int>(b), lut.get(), stream));
-        });
-        vk::ThreadScanArgs a{lut.get(), codes_il.get(), codes_v.get(), static_cast<int64_t>(n), static_cast<int>(m),
-                             static_cast<int>(b), part.get()};
-        clock.time(&t->scan_ms, [&] {
-            VK_HIP(kern.launch(a, dim3(static_cast<unsigned>(bx), static_cast<unsigned>(b)), smem, stream));
-        });
-        vk::SelectArgs s{};
-        s.mode = 1;
-        s.part = part.get();
-        s.K = K;
-        s.bx = bx;
-        s.k = static_cast<int>(kk);
-        s.out = d_out;
-        clock.time(&t->select_ms, [&] { VK_HIP(vk::launch_select(s, static_cast<int>(b), stream)); });
-    }
-
     // v5-v7: per-thread-list fused scans on a (blocks_x, query groups) grid, then the final merge.
     void run_thread(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
         const int K = vk::plan::dispatched_k(kk);
@@ -508,13 +464,16 @@ struct vk_searcher {
     void run_variant(int v, const float* d_q, size_t b, size_t kk, Pair* d_out, vk_timings* t, StageClock& clock) {
         if (v == VK_V8_FUSED_WARP || v == VK_V9_FUSED_WARP_F16)
             return run_wave(d_q, b, kk, v == VK_V9_FUSED_WARP_F16, d_out, t, clock);
-        if (v == VK_V4_FUSED) return run_list(d_q, b, kk, d_out, t, clock);
         if (vk_is_fused(v)) return run_thread(v, d_q, b, kk, d_out, t, clock);
         run_unfused(v, d_q, b, kk, d_out, t, clock);
     }
 
     void check_search(size_t kk, int v) const {
         require(valid_variant(v), "unknown scan variant " + std::to_string(v));
+        if (v == VK_V4_FUSED)
+            fail(VK_ERR_LOGIC,
+                 "v4_fused is not launched in this build: its run-time-indexed per-thread list faulted the GPU "
+                 "(memory-aperture violation, cause not established); use v5_fused_reg or later");
         require(kk >= 1 && kk <= 128 && kk <= n, "k must be in [1, min(128, n)]");
         validate(v);
     }

@@ -138,13 +138,6 @@ struct ThreadScanKernel {
 
 // The instance for a variant (5-7), list length K and the effective Q (v7) and ILP (v6, v7).
 ThreadScanKernel fused_thread_kernel(int variant, int K, int q, int ilp);
-// v4: per-thread lists in LDS, grid (blocks_x, nq), `threads` in {64, 128, 256}. Dynamic LDS bytes:
-// m * 256 * 4 (table) + threads * K * 8 (lists) + (threads / 64 + 1) * K * 8 (merge).
-ThreadScanKernel fused_list_kernel(int K, int threads);
-inline size_t fused_list_lds(int m, int K, int threads) {
-    return static_cast<size_t>(m) * KSUB * sizeof(float) + static_cast<size_t>(threads) * K * 8 +
-           static_cast<size_t>(threads / WAVE + 1) * K * sizeof(Pair);
-}
 
 // ---- selection / final merge (select.hip)
 struct SelectArgs {

@@ -4,12 +4,12 @@
 //   v1 SharedLut     LUT staged in LDS
 //   v2 SharedLutVec  16-byte row loads (m % 16 == 0)
 //   v3 Interleaved   byte-interleaved wave64 tiles: code s of 64 consecutive vectors is 64 contiguous bytes
-//   v4 Fused         one vector per thread over the byte-interleaved tiles, a sorted K-list per thread kept in
-//                    LDS and updated by run-time-length shifts (the reference's list_insert)
+//   v4 Fused         not launched: its run-time-indexed per-thread list faulted the GPU with a memory-aperture
+//                    violation whose cause is not established; the host rejects v4 before any launch
 //   v5 FusedReg      per-thread list updated with compile-time indices only, so it stays in registers
 //   v6 FusedVec      v5 over 16-byte-word-interleaved tiles, ILP vectors per thread per step
 //   v7 FusedVecMQ    v6 with Q queries per block sharing each code load (Q * K <= 64)
-// v0-v3 write the nq x n distance matrix, reduced by the select kernel; v4-v7 emit one partial K-list per
+// v0-v3 write the nq x n distance matrix, reduced by the select kernel; v5-v7 emit one partial K-list per
 // (query, block), reduced by the select kernel. Distances are summed in sub-space order s = 0..m-1 from 0.f,
 // like the CPU reference, so every variant is bit-exact against it.
 #include "kernels.hpp"
@@ -74,113 +74,6 @@ hipError_t launch_scan(int variant, const ScanArgs& a, int blocks_x, int nq, int
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
-}
-
-// ---------------------------------------------------------------- v4: per-thread lists in LDS
-
-// grid (blocks_x, nq), T threads, one query per block row (kernels.cuh:207-230). Each thread scans vectors
-// i = blockIdx.x * T + tid + j * gridDim.x * T of the byte-interleaved tiles and keeps its K best in LDS, in two
-// planes of K rows of T entries (distance, id): entry j of thread t sits at [j * T + t], so at any list index the 64
-// lanes of a wave touch 64 consecutive dwords (no bank conflicts however far each lane's insertion shifts). An
-// insertion walks back from the end while the candidate precedes the entry in (dist, id) order, moving entries
-// one place down, as list_insert does (kernels.cuh:127-138); the thread's K-th entry is kept in registers, so a
-// candidate that does not enter costs no LDS access. The lists never leave LDS (no scratch, no generic pointers).
-// After the scan each wave streams its 64 lanes' lists into a wave list (entry j of every lane at a time: each
-// lane's entries ascend and the threshold only falls, so once no lane's entry j is admitted none of its later
-// entries is), and the W wave lists are merged by rank into the block's partial list.
-// Dynamic LDS: the query's table (m * 256 floats), the two list planes (T * K * 8 bytes), then W + 1 pair lists.
-template <int K, int T>
-__global__ void __launch_bounds__(T) fused_list_kernel_t(ThreadScanArgs a) {
-    constexpr int W = T / WAVE, S = K <= WAVE ? 1 : 2;
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int m = a.m, tsize = m * KSUB;
-    float* table = reinterpret_cast<float*>(smem);
-    float* list_d = table + tsize;
-    int32_t* list_i = reinterpret_cast<int32_t*>(list_d + K * T);
-    Pair* buf = reinterpret_cast<Pair*>(list_i + K * T);
-    const int tid = threadIdx.x, wave = tid / WAVE;
-    const int64_t q = blockIdx.y;
-    for (int j = tid; j < tsize; j += T) table[j] = a.lut[q * tsize + j];
-    for (int j = 0; j < K; ++j) {
-        list_d[j * T + tid] = INFINITY;
-        list_i[j * T + tid] = kEmptyId;
-    }
-    __syncthreads();
-
-    float worst_d = INFINITY;  // the thread's entry K - 1
-    int32_t worst_i = kEmptyId;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * T;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * T + tid; i < a.n; i += stride) {
-        const uint8_t* tile = a.codes_il + (i >> 6) * m * WAVE + (i & 63);
-        float acc = 0.f;
-        for (int s = 0; s < m; ++s) acc += table[s * KSUB + tile[s * WAVE]];
-        const int32_t id = static_cast<int32_t>(i);
-        if (!pair_less(acc, id, worst_d, worst_i)) continue;
-        int j = K - 1;
-        while (j > 0) {
-            const float pd = list_d[(j - 1) * T + tid];
-            const int32_t pi = list_i[(j - 1) * T + tid];
-            if (!pair_less(acc, id, pd, pi)) break;
-            list_d[j * T + tid] = pd;
-            list_i[j * T + tid] = pi;
-            --j;
-        }
-        list_d[j * T + tid] = acc;
-        list_i[j * T + tid] = id;
-        worst_d = list_d[(K - 1) * T + tid];
-        worst_i = list_i[(K - 1) * T + tid];
-    }
-
-    WaveList<S> wl;
-    wl.init();
-    for (int j = 0; j < K; ++j) {
-        const float dj = list_d[j * T + tid];
-        const int32_t ij = list_i[j * T + tid];
-        const bool valid = ij != kEmptyId;
-        if (__builtin_amdgcn_ballot_w64(valid && dj <= wl.thr_d) == 0) break;
-        wl.offer(dj, ij, valid, K);
-    }
-    Pair* merged = buf + W * K;
-    wl.store(buf + wave * K, K);
-    __syncthreads();
-    merge_lists(buf, W, K, merged, tid, T);
-    __syncthreads();
-    Pair* dst = a.part + (q * gridDim.x + blockIdx.x) * static_cast<int64_t>(K);
-    for (int j = tid; j < K; j += T) dst[j] = merged[j];
-}
-
-template <int K, int T>
-hipError_t launch_fused_list_t(const ThreadScanArgs& a, dim3 grid, size_t smem, hipStream_t stream) {
-    hipLaunchKernelGGL((fused_list_kernel_t<K, T>), grid, dim3(T), smem, stream, a);
-    return hipGetLastError();
-}
-
-template <int K, int T>
-ThreadScanKernel make_list_kernel() {
-    ThreadScanKernel k;
-    k.fn = reinterpret_cast<const void*>(&fused_list_kernel_t<K, T>);
-    k.threads = T;
-    k.launch = &launch_fused_list_t<K, T>;
-    return k;
-}
-
-template <int K>
-ThreadScanKernel list_kernel_for_k(int threads) {
-    if (threads == 256) return make_list_kernel<K, 256>();
-    if (threads == 128) return make_list_kernel<K, 128>();
-    if (threads == 64) return make_list_kernel<K, 64>();
-    return ThreadScanKernel{};
-}
-
-ThreadScanKernel fused_list_kernel(int K, int threads) {
-    switch (K) {
-        case 8: return list_kernel_for_k<8>(threads);
-        case 16: return list_kernel_for_k<16>(threads);
-        case 32: return list_kernel_for_k<32>(threads);
-        case 64: return list_kernel_for_k<64>(threads);
-        case 128: return list_kernel_for_k<128>(threads);
-        default: return ThreadScanKernel{};
-    }
 }
 
 // ---------------------------------------------------------------- v5 - v7: per-thread register lists
@@ -321,7 +214,7 @@ ThreadScanKernel vec_kernel(int ilp) {
 
 template <int K>
 ThreadScanKernel thread_kernel_for_k(int variant, int q, int ilp) {
-    if (variant == 4) return ThreadScanKernel{};  // v4: fused_list_kernel
+    if (variant == 4) return ThreadScanKernel{};  // v4 is not launched (see the header of this file)
     if (variant == 5) return make_thread_kernel<K, 1, 1, false>();
     if (variant == 6 || q <= 1) return vec_kernel<K, 1>(ilp);
     if constexpr (K <= 8) {
