@@ -149,6 +149,23 @@ int vk_distances(vk_searcher* s, const float* queries, size_t nq, int variant, f
 int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq, size_t k, int variant, vk_neighbor* d_out,
                      vk_timings* timings);
 
+/* Allocation-free device-resident search. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory during a search (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and errors as vk_search_device for v8_fused_warp and v9_fused_warp_f16 (other variants:
+ * VK_ERR_INVALID_ARGUMENT), but the partial lists and slab counters live in a static device array of
+ * VK_NOALLOC_SCRATCH_BYTES that the library holds on each device it runs on until the process ends (the first
+ * VK_NOALLOC_COUNTER_BYTES for the counters, one 4-byte counter per slab of queries_per_block queries; the rest for
+ * the partial lists), so the call makes no device allocation, creates no events and records no timings. A search
+ * needing more than that (very large nq x k) is rejected before any launch with VK_ERR_INVALID_ARGUMENT; split it
+ * into smaller calls. The searcher's word-interleaved code layout must already exist: one vk_search or
+ * vk_search_device call with v8 or v9 builds it (that call allocates); otherwise VK_ERR_LOGIC. Calls on one device
+ * share its array: the library serialises them within a process (a per-device lock held until the call's stream
+ * has finished), and overlapping calls would otherwise race on it. Synchronous, like vk_search_device. */
+#define VK_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+#define VK_NOALLOC_COUNTER_BYTES ((size_t)64 << 10)
+int vk_search_device_noalloc(vk_searcher* s, const float* d_queries, size_t nq, size_t k, int variant,
+                             vk_neighbor* d_out);
+
 /* Exact re-ranking on the GPU: replaces rerank_exact (cpu_ref.hpp:55-56, cpu_ref.cpp:66-77), the step after the
  * search that bench --rerank R runs (bench_main.cpp:145-153). The reference re-ranks on the CPU from host arrays;
  * here the n x d base vectors are copied to the current device once by vk_reranker_create, and each call scores

@@ -111,6 +111,7 @@ _SIGNATURES = {
     "vk_distances": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P, ctypes.POINTER(_Timings)]),
     "vk_search_device": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P,
                                         ctypes.POINTER(_Timings)]),
+    "vk_search_device_noalloc": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P]),
     "vk_ivf_create": (ctypes.c_int, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, ctypes.c_size_t, _P, _P,
                                      ctypes.c_size_t, ctypes.POINTER(_P)]),
     "vk_ivf_destroy": (None, [_P]),
@@ -340,6 +341,11 @@ class PQSearcher:
         _check(library().vk_search_device(self._h, ctypes.c_void_p(d_queries), nq, k, int(variant),
                                           ctypes.c_void_p(d_out), ctypes.byref(t)))
         return _timings(t)
+
+    def search_device_noalloc(self, d_queries: int, nq: int, k: int, variant: int, d_out: int) -> None:
+        """search_device without any device allocation (v8 / v9): scratch is the library's static device array."""
+        _check(library().vk_search_device_noalloc(self._h, ctypes.c_void_p(d_queries), nq, k, int(variant),
+                                                  ctypes.c_void_p(d_out)))
 
 
 def pq_encode(centroids: np.ndarray, x: np.ndarray) -> np.ndarray:

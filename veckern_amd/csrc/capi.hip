@@ -9,6 +9,7 @@
 #include <cstring>
 #include <limits>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -48,6 +49,15 @@ WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, b
     }
 }
 }  // namespace vk
+
+// Scratch of the allocation-free search (vk_search_device_noalloc): a fixed device array that the code object
+// carries, so that entry point never allocates. Each device holds its own copy for the life of the process. Layout:
+// the per-slab completion counters in the first kNoAllocCounterBytes (kept at zero between searches: the kernel
+// leaves them there), then the partial lists. Host code never names `scratch` as a device address: it uses the
+// per-device address that hipGetSymbolAddress returns (noalloc_device below).
+constexpr size_t kNoAllocScratchBytes = VK_NOALLOC_SCRATCH_BYTES;
+constexpr size_t kNoAllocCounterBytes = VK_NOALLOC_COUNTER_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -215,6 +225,17 @@ void fill_device_info(int device, vk_device_info* out) {
     out->l2_bytes = static_cast<size_t>(p.l2CacheSize);
     out->total_mem_bytes = p.totalGlobalMem;
 }
+
+// Per-device state of the allocation-free search. `lock` serialises its calls on one device (they share the
+// device's scratch array); `base` is the array's address on that device, found once with the device current.
+struct NoAllocDevice {
+    std::mutex lock;
+    bool found = false;
+    bool counters_clean = false;  // false until zeroed, and after a call that stopped between launch and completion
+    unsigned char* base = nullptr;
+};
+constexpr int kNoAllocMaxDevices = 64;
+NoAllocDevice g_noalloc[kNoAllocMaxDevices];
 
 }  // namespace
 
@@ -551,6 +572,57 @@ struct vk_searcher {
             clock.settle();
             counters_dirty = false;
         }
+    }
+
+    // search_device for v8 / v9 with the device's static scratch array instead of the searcher's buffers: no
+    // allocation (device or host, outside error messages), no events. Every batch's scratch need is checked before
+    // the first launch; a batch is planned again at its launch (the plan is a pure function of the batch size).
+    void search_device_noalloc(const float* d_q, size_t nq, size_t kk, int v, vk_neighbor* d_out) {
+        check_search(kk, v);
+        if (v != VK_V8_FUSED_WARP && v != VK_V9_FUSED_WARP_F16)
+            fail(VK_ERR_INVALID_ARGUMENT, "vk_search_device_noalloc runs v8_fused_warp and v9_fused_warp_f16 only");
+        if (!have_v)
+            fail(VK_ERR_LOGIC, "the searcher's word-interleaved code layout is not built yet: one vk_search or "
+                               "vk_search_device call with v8 or v9 builds it (that call allocates)");
+        require(device >= 0 && device < kNoAllocMaxDevices, "device index out of range for the static scratch");
+        use_device();
+        const bool f16 = v == VK_V9_FUSED_WARP_F16;
+        const size_t batch = query_batch(v);
+        for (size_t q0 = 0; q0 < nq; q0 += batch) {
+            const WavePlan w = plan_wave(std::min(batch, nq - q0), kk, f16);
+            const size_t counter_bytes = static_cast<size_t>(w.part.slabs) * sizeof(unsigned);
+            const size_t part_bytes = w.part_pairs * sizeof(Pair);
+            if (counter_bytes > kNoAllocCounterBytes || part_bytes > kNoAllocScratchBytes - kNoAllocCounterBytes)
+                fail(VK_ERR_INVALID_ARGUMENT,
+                     "vk_search_device_noalloc: this search needs " + std::to_string(part_bytes) +
+                         " bytes of partial lists and " + std::to_string(counter_bytes) +
+                         " bytes of slab counters, beyond its static scratch (" +
+                         std::to_string(kNoAllocScratchBytes - kNoAllocCounterBytes) + " and " +
+                         std::to_string(kNoAllocCounterBytes) + " bytes); search fewer queries per call");
+        }
+        NoAllocDevice& dev = g_noalloc[device];
+        std::lock_guard<std::mutex> hold(dev.lock);
+        if (!dev.found) {
+            void* p = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || p == nullptr)
+                fail(VK_ERR_DEVICE, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+            dev.base = static_cast<unsigned char*>(p);
+            dev.found = true;
+        }
+        unsigned* counter_buf = reinterpret_cast<unsigned*>(dev.base);
+        Pair* part_buf = reinterpret_cast<Pair*>(dev.base + kNoAllocCounterBytes);
+        if (!dev.counters_clean)
+            VK_HIP(vk::launch_zero_words(counter_buf, static_cast<int64_t>(kNoAllocCounterBytes / sizeof(unsigned)),
+                                         stream));
+        dev.counters_clean = false;  // until the stream has completed every launch below
+        for (size_t q0 = 0; q0 < nq; q0 += batch) {
+            const size_t b = std::min(batch, nq - q0);
+            launch_wave(plan_wave(b, kk, f16), d_q + q0 * d, b, kk, reinterpret_cast<Pair*>(d_out + q0 * kk),
+                        part_buf, counter_buf);
+        }
+        VK_HIP(hipStreamSynchronize(stream));
+        dev.counters_clean = true;
     }
 };
 
@@ -1197,6 +1269,19 @@ VK_EXPORT int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq
             s->check_search(k, variant);
         }
         if (timings) *timings = t;
+    });
+}
+
+VK_EXPORT int vk_search_device_noalloc(vk_searcher* s, const float* d_queries, size_t nq, size_t k, int variant,
+                                       vk_neighbor* d_out) {
+    return guarded([&] {
+        require(s != nullptr, "searcher is null");
+        if (nq > 0) {
+            require(d_queries != nullptr && d_out != nullptr, "queries and out must not be null");
+            s->search_device_noalloc(d_queries, nq, k, variant, d_out);
+        } else {
+            s->check_search(k, variant);
+        }
     });
 }
 

@@ -21,6 +21,8 @@ hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_
 // Byte-interleaved: out[(tile * m + s) * 64 + lane] = sub-code s of vector tile*64+lane.
 hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint8_t* out,
                               hipStream_t stream);
+// Zeroes count 32-bit words with a kernel (no memset node).
+hipError_t launch_zero_words(unsigned* p, int64_t count, hipStream_t stream);
 
 // ---- fused scan with wave-cooperative lists (fused_wave_*.hip)
 struct WaveScanArgs {

@@ -47,4 +47,18 @@ hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_
     return hipGetLastError();
 }
 
+// Sets count words to zero with vector stores (used where a hipMemsetAsync node is unwanted, e.g. in work a
+// caller may capture into a graph).
+__global__ void __launch_bounds__(256) zero_words_kernel(unsigned* __restrict__ p, int64_t count) {
+    for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < count;
+         o += static_cast<int64_t>(gridDim.x) * 256)
+        p[o] = 0u;
+}
+
+hipError_t launch_zero_words(unsigned* p, int64_t count, hipStream_t stream) {
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(layout_grid(count)), dim3(256), 0, stream, p, count);
+    return hipGetLastError();
+}
+
 }  // namespace vk
