@@ -389,13 +389,20 @@ __global__ void __launch_bounds__(T)
     // SIMD to finish the block, too few to keep the LDS pipe busy.
     __shared__ unsigned next_gran;
     __shared__ unsigned qmax[QS];  // fp16 tables: per-query maximum entry of the current slab (raw bits)
-    // Long lists (K > 64) only: per (query, wave), the distance of the wave list's entry ceil(K/W) - 1 for the
-    // current slab (raw bits of a distance >= 0, so unsigned order is float order; +inf until the list holds that
-    // many). If every wave holds ceil(K/W) entries at or below T, the block holds at least K, so the maximum over
-    // the waves bounds the block's K-th best: a candidate beyond it cannot reach the merged top K, and every wave
-    // filters by it. At K = 128 this removes ~40 % of the inserts; at K <= 64 the bookkeeping costs more than
-    // the inserts it saves.
-    constexpr bool kShareBound = S > 1;
+    // Long lists (K > 64), and the bulk instances (few vectors per block): per (query, wave), the distance of the
+    // wave list's entry ceil(K/W) - 1 for the current slab (raw bits of a distance >= 0, so unsigned order is float
+    // order; +inf until the list holds that many). If every wave holds ceil(K/W) entries at or below T, the block
+    // holds at least K, so the maximum over the waves bounds the block's K-th best: a candidate beyond it cannot
+    // reach the merged top K, and every wave filters by it. At K = 128 this removes ~40 % of the inserts. For
+    // one-register lists over many vectors per block the bookkeeping costs more than the inserts it saves
+    // (measured with the lane-parallel form below: 1M x nq=1000 +0.5 %, 10M +0.8 %, fp16 tables at 8 queries
+    // +4.7 %); with few vectors per block, where a larger share of the candidates enters fresh lists, it pays
+    // (100k x nq=100: -2 %).
+    constexpr bool kShareBound = S > 1 || (BULK && !IVF);
+    // When every (query, wave) slot fits in one wave, a step reads all of them with one LDS read (lane l: slot l)
+    // and takes each query's maximum over its W lanes by DPP exchanges; a wave publishes its QS values with one
+    // LDS write (lane q: query q), always (they only fall).
+    constexpr bool kLaneBound = kShareBound && QS * W <= WAVE && (W == 2 || W == 4 || W == 8);
     __shared__ __align__(16) unsigned rank_bound[QS][W];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
@@ -523,7 +530,12 @@ __global__ void __launch_bounds__(T)
             if constexpr (!IVF)
                 if (lane == 0) grab = atomicAdd(&next_gran, 1u);
             // The block's bound per query (a stale slot only loosens it: published values only fall).
-            if constexpr (kShareBound) {
+            // Lane-parallel form: the slots are read here and used only after the first tile's lookups (a wait for
+            // this read right away would queue behind the CU's random table reads).
+            int bound_raw = 0;
+            if constexpr (kLaneBound) {
+                bound_raw = lane < QS * W ? static_cast<int>((&rank_bound[0][0])[lane]) : 0;
+            } else if constexpr (kShareBound) {
 #pragma unroll
                 for (int q = 0; q < QS; ++q) {
                     unsigned mx = 0u;
@@ -616,6 +628,16 @@ __global__ void __launch_bounds__(T)
                     for (int w = 0; w < words; ++w) lookup_word(tile_codes[(u * words + w) * WAVE], w);
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                if constexpr (kLaneBound) {
+                    if (u == 0) {  // raw bits of distances >= 0 or +inf: signed order is float order
+                        int mx = max(bound_raw, xor_lane<1>(bound_raw));
+                        if constexpr (W > 2) mx = max(mx, xor_lane<2>(mx));
+                        if constexpr (W > 4) mx = max(mx, xor_lane<4>(mx));
+#pragma unroll
+                        for (int q = 0; q < QS; ++q)
+                            lists[q].set_cap(__int_as_float(__builtin_amdgcn_readlane(mx, q * W)));
+                    }
+                }
                 // Lanes holding a real vector: all of them except in the database's last tile (or, for inverted
                 // lists, the padding at the end of each list).
                 uint32_t id;
@@ -636,7 +658,15 @@ __global__ void __launch_bounds__(T)
                 }
             }
             // Publish this wave's entry ceil(K/W) - 1 when it has fallen.
-            if constexpr (kShareBound) {
+            if constexpr (kLaneBound) {
+                int pub = 0;
+#pragma unroll
+                for (int q = 0; q < QS; ++q) {
+                    const int v = __float_as_int(lane_read(lists[q].d[0], bound_rank));
+                    pub = lane == q ? v : pub;
+                }
+                if (lane < QS) rank_bound[lane][wave] = static_cast<unsigned>(pub);
+            } else if constexpr (kShareBound) {
 #pragma unroll
                 for (int q = 0; q < QS; ++q) {
                     const float v = lane_read(lists[q].d[0], bound_rank);
