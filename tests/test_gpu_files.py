@@ -78,3 +78,22 @@ def test_bvecs_inputs(tmp_path):
     fp32, fp16 = expected_recalls(base, queries, truth)
     assert float(rows["v8_fused_warp"]["recall"]) == pytest.approx(fp32, abs=1e-6)
     assert float(rows["v9_fused_warp_f16"]["recall"]) == pytest.approx(fp16, abs=1e-6)
+
+
+def test_default_variant_list_runs_every_launched_variant(tmp_path):
+    # `--variants all` (the reference's default): one row per variant this build launches, v4 reported without a row
+    # (it is rejected before launch), plus the CPU search path's row; every GPU row scores the CPU row's recall
+    out = str(tmp_path / "all.csv")
+    cmd = [EXE, "--n", "60000", "--d", "64", "--m", "16", "--nq", "40", "--k", "10", "--train", "5000", "--iters", "3",
+           "--reps", "1", "--eval-queries", "40", "--cpu-queries", "40", "--csv", out, "--label", "all"]
+    print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    print(r.stdout[-3000:])
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+    assert "v4_fused: no row" in r.stdout
+    rows = list(csv.DictReader(open(out)))
+    assert [row["variant"] for row in rows] == ["cpu_reference", "v0_global_lut", "v1_shared_lut", "v2_shared_lut_vec",
+                                                "v3_interleaved", "v5_fused_reg", "v6_fused_vec", "v7_fused_vec_mq",
+                                                "v8_fused_warp"]
+    cpu = float(rows[0]["recall"])
+    assert all(float(row["recall"]) == pytest.approx(cpu, abs=1e-9) for row in rows), rows
