@@ -242,8 +242,9 @@ def main():
     ap.add_argument("--config", default="B", choices=sorted(CONFIGS))
     ap.add_argument("--variant", default="v8")
     ap.add_argument("--queries-per-block", type=int, default=None,
-                    help="Q (default 2 for config A, whose 100k-vector slabs give a block too little to scan for "
-                         "4 queries' tables; 4 otherwise)")
+                    help="Q (default 8 for the fp16-table variant v9, whose 16-byte reads hold 8 queries' entries; "
+                         "2 for config A, whose 100k-vector slabs give a block too little to scan for 4 queries' "
+                         "tables; 4 otherwise)")
     ap.add_argument("--ilp", type=int, default=4)
     ap.add_argument("--blocks-per-query", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and its parity check")
@@ -284,8 +285,8 @@ def main():
         + f"; HBM read {hbm_gbs:.0f} GB/s")
 
     s = vk.PQSearcher(centroids, codes, d)
-    if args.queries_per_block is None:
-        args.queries_per_block = 2 if args.config == "A" else 4
+    if args.queries_per_block is None:  # fp16 tables: 8 queries share one 16-byte table read
+        args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config == "A" else 4)
     s.set_tuning(vk.Tuning(queries_per_block=args.queries_per_block, vectors_per_step=args.ilp,
                            blocks_per_query=args.blocks_per_query))
     dq = vk.DeviceArray.from_host(queries)
