@@ -168,6 +168,11 @@ public:
     ~StageClock() {
         for (auto& e : events_) (void)hipEventDestroy(e);
     }
+    // Forgets stages recorded by a call that did not reach settle() (it raised); the events are kept for reuse.
+    void reset() {
+        pending_.clear();
+        used_ = 0;
+    }
     template <typename F>
     void time(double* acc, F&& work) {
         hipEvent_t a = next(), b = next();
@@ -257,8 +262,10 @@ struct vk_searcher {
     size_t counters_zeroed = 0;
     bool counters_dirty = false;
     bool have_il = false, have_v = false;
+    std::unique_ptr<StageClock> clock_pool;
 
     ~vk_searcher() {
+        clock_pool.reset();  // its events before the stream
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -271,17 +278,25 @@ struct vk_searcher {
     }
 
     void ensure_layout(int v) {
+        bool built = false;
         if (vk::plan::uses_byte_layout(v) && !have_il) {
             codes_il.ensure(static_cast<size_t>(n_pad) * m);
             VK_HIP(vk::launch_build_bytes(codes.get(), n, static_cast<int>(m), n_pad, codes_il.get(), stream));
-            have_il = true;
+            have_il = built = true;
         }
         if (vk::plan::uses_word_layout(v) && !have_v) {
             codes_v.ensure(static_cast<size_t>(n_pad) * (m / 16));
             VK_HIP(vk::launch_build_words(codes.get(), n, static_cast<int>(m), n_pad, codes_v.get(), stream));
-            have_v = true;
+            have_v = built = true;
         }
-        VK_HIP(hipStreamSynchronize(stream));
+        if (built) VK_HIP(hipStreamSynchronize(stream));  // a layout kernel's failure surfaces here, not mid-search
+    }
+
+    // The stage clock of this searcher's calls: its events are created once and reused by every call.
+    StageClock& stage_clock() {
+        if (!clock_pool) clock_pool = std::make_unique<StageClock>(stream);
+        clock_pool->reset();
+        return *clock_pool;
     }
 
     // v8 / v9 (f16 tables): the wave-list scan over the balanced partition with its final merge, one launch. The
@@ -514,7 +529,7 @@ struct vk_searcher {
         validate(v);
         use_device();
         ensure_layout(v);
-        StageClock clock(stream);
+        StageClock& clock = stage_clock();
         const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
             const size_t b = std::min(batch, nq - q0);
@@ -536,7 +551,7 @@ struct vk_searcher {
         check_search(kk, v);
         use_device();
         ensure_layout(v);
-        StageClock clock(stream);
+        StageClock& clock = stage_clock();
         const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
             const size_t b = std::min(batch, nq - q0);
@@ -564,7 +579,7 @@ struct vk_searcher {
         check_search(kk, v);
         use_device();
         ensure_layout(v);
-        StageClock clock(stream);
+        StageClock& clock = stage_clock();
         const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
             const size_t b = std::min(batch, nq - q0);
