@@ -62,45 +62,53 @@ __device__ __forceinline__ int xor_lane(int v) {
     }
 }
 
-// Compare-exchange of a lane's pair with the pair of lane ^ J: the lane keeps the smaller of the two under the
-// (dist, id) order when keep_min, else the larger. Both lanes of an exchange decide consistently, so the two pairs
-// are kept, never duplicated (identical pairs, i.e. empty slots, may swap harmlessly). Branch-free: the order test
-// uses non-short-circuit operators so that it becomes compares and selects.
+// A pair as one 64-bit key: the distance's bits above, the id below. For the pairs a wave list holds -- distances
+// >= +0 or +inf (a NaN distance is never admitted: no comparison with it holds) and ids >= 0 or kEmptyId -- the
+// unsigned order of the keys is the (dist, id) order, so the sorting networks below compare pairs with one 64-bit
+// compare instead of three 32-bit ones.
+__device__ __forceinline__ uint64_t pair_key(float d, int32_t i) {
+    return (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<uint32_t>(i);
+}
+__device__ __forceinline__ float key_dist(uint64_t k) { return __uint_as_float(static_cast<uint32_t>(k >> 32)); }
+__device__ __forceinline__ int32_t key_id(uint64_t k) { return static_cast<int32_t>(static_cast<uint32_t>(k)); }
+constexpr uint64_t kEmptyKey = (uint64_t{0x7f800000u} << 32) | static_cast<uint32_t>(kEmptyId);  // (+inf, kEmptyId)
+
+// Compare-exchange of a lane's key with the key of lane ^ J: the lane keeps the smaller of the two when keep_min,
+// else the larger. Both lanes of an exchange decide consistently, so the two keys are kept, never duplicated.
 template <int J>
-__device__ __forceinline__ void exchange_xor(float& d, int32_t& i, bool keep_min) {
-    const float pd = __int_as_float(xor_lane<J>(__float_as_int(d)));
-    const int32_t pi = xor_lane<J>(i);
-    const bool less = (pd < d) | ((pd == d) & (pi < i));
-    const bool take = less == keep_min;
-    d = take ? pd : d;
-    i = take ? pi : i;
+__device__ __forceinline__ void exchange_xor(uint64_t& k, bool keep_min) {
+    const int lo = xor_lane<J>(static_cast<int>(static_cast<uint32_t>(k)));
+    const int hi = xor_lane<J>(static_cast<int>(static_cast<uint32_t>(k >> 32)));
+    const uint64_t pk = (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+    const bool take = (pk < k) == keep_min;
+    k = take ? pk : k;
 }
 
-// Bitonic sort of one pair per lane, ascending by lane, or descending with DESC (21 compare-exchange steps).
+// Bitonic sort of one key per lane, ascending by lane, or descending with DESC (21 compare-exchange steps).
 template <int K = 2, bool DESC = false>
-__device__ __forceinline__ void wave_sort(float& d, int32_t& i) {
+__device__ __forceinline__ void wave_sort(uint64_t& k) {
     if constexpr (K <= WAVE) {
         const int lane = __lane_id();
         const bool up = K == WAVE ? !DESC : (lane & K) == 0;
-        if constexpr (K >= 64) exchange_xor<32>(d, i, ((lane & 32) == 0) == up);
-        if constexpr (K >= 32) exchange_xor<16>(d, i, ((lane & 16) == 0) == up);
-        if constexpr (K >= 16) exchange_xor<8>(d, i, ((lane & 8) == 0) == up);
-        if constexpr (K >= 8) exchange_xor<4>(d, i, ((lane & 4) == 0) == up);
-        if constexpr (K >= 4) exchange_xor<2>(d, i, ((lane & 2) == 0) == up);
-        exchange_xor<1>(d, i, ((lane & 1) == 0) == up);
-        wave_sort<K * 2, DESC>(d, i);
+        if constexpr (K >= 64) exchange_xor<32>(k, ((lane & 32) == 0) == up);
+        if constexpr (K >= 32) exchange_xor<16>(k, ((lane & 16) == 0) == up);
+        if constexpr (K >= 16) exchange_xor<8>(k, ((lane & 8) == 0) == up);
+        if constexpr (K >= 8) exchange_xor<4>(k, ((lane & 4) == 0) == up);
+        if constexpr (K >= 4) exchange_xor<2>(k, ((lane & 2) == 0) == up);
+        exchange_xor<1>(k, ((lane & 1) == 0) == up);
+        wave_sort<K * 2, DESC>(k);
     }
 }
 
-// Sorts a bitonic sequence of one pair per lane ascending (6 compare-exchange steps).
-__device__ __forceinline__ void wave_clean(float& d, int32_t& i) {
+// Sorts a bitonic sequence of one key per lane ascending (6 compare-exchange steps).
+__device__ __forceinline__ void wave_clean(uint64_t& k) {
     const int lane = __lane_id();
-    exchange_xor<32>(d, i, (lane & 32) == 0);
-    exchange_xor<16>(d, i, (lane & 16) == 0);
-    exchange_xor<8>(d, i, (lane & 8) == 0);
-    exchange_xor<4>(d, i, (lane & 4) == 0);
-    exchange_xor<2>(d, i, (lane & 2) == 0);
-    exchange_xor<1>(d, i, (lane & 1) == 0);
+    exchange_xor<32>(k, (lane & 32) == 0);
+    exchange_xor<16>(k, (lane & 16) == 0);
+    exchange_xor<8>(k, (lane & 8) == 0);
+    exchange_xor<4>(k, (lane & 4) == 0);
+    exchange_xor<2>(k, (lane & 2) == 0);
+    exchange_xor<1>(k, (lane & 1) == 0);
 }
 
 // One sorted list of up to 64*S (dist, id) pairs spread over a wave: entry p lives in lane p % 64, register
@@ -236,12 +244,12 @@ struct WaveList {
     // bitonic sequence holding the 64*S smallest pairs of both; a bitonic clean sorts it. The result is the list
     // the one-by-one inserts would give.
     __device__ __forceinline__ void merge_wave(float x, int32_t xi, bool offered, int K) {
-        float cd = offered ? x : INFINITY;
-        int32_t ci = offered ? xi : kEmptyId;
-        wave_sort<2, true>(cd, ci);
-        const bool less = (cd < d[S - 1]) | ((cd == d[S - 1]) & (ci < id[S - 1]));
-        d[S - 1] = less ? cd : d[S - 1];
-        id[S - 1] = less ? ci : id[S - 1];
+        uint64_t c = offered ? pair_key(x, xi) : kEmptyKey;
+        wave_sort<2, true>(c);
+        const uint64_t last = pair_key(d[S - 1], id[S - 1]);
+        const uint64_t low = c < last ? c : last;
+        d[S - 1] = key_dist(low);
+        id[S - 1] = key_id(low);
         clean(K);
     }
 
@@ -266,30 +274,35 @@ struct WaveList {
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const bool less = (cd[s] < d[s]) | ((cd[s] == d[s]) & (ci[s] < id[s]));
-            d[s] = less ? cd[s] : d[s];
-            id[s] = less ? ci[s] : id[s];
+            const uint64_t c = pair_key(cd[s], ci[s]), own = pair_key(d[s], id[s]);
+            const uint64_t low = c < own ? c : own;
+            d[s] = key_dist(low);
+            id[s] = key_id(low);
         }
         clean(K);
     }
 
     // Sorts the list after an elementwise minimum left it bitonic, and reads the new threshold.
     __device__ __forceinline__ void clean(int K) {
+        uint64_t k[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) k[s] = pair_key(d[s], id[s]);
 #pragma unroll
         for (int h = S / 2; h > 0; h >>= 1)  // register distances (S is a power of two)
 #pragma unroll
             for (int s = 0; s < S; ++s)
                 if ((s & h) == 0) {
-                    const bool swap = (d[s + h] < d[s]) | ((d[s + h] == d[s]) & (id[s + h] < id[s]));
-                    const float lo_d = swap ? d[s + h] : d[s], hi_d = swap ? d[s] : d[s + h];
-                    const int32_t lo_i = swap ? id[s + h] : id[s], hi_i = swap ? id[s] : id[s + h];
-                    d[s] = lo_d;
-                    id[s] = lo_i;
-                    d[s + h] = hi_d;
-                    id[s + h] = hi_i;
+                    const bool swap = k[s + h] < k[s];
+                    const uint64_t lo = swap ? k[s + h] : k[s], hi = swap ? k[s] : k[s + h];
+                    k[s] = lo;
+                    k[s + h] = hi;
                 }
 #pragma unroll
-        for (int s = 0; s < S; ++s) wave_clean(d[s], id[s]);
+        for (int s = 0; s < S; ++s) {
+            wave_clean(k[s]);
+            d[s] = key_dist(k[s]);
+            id[s] = key_id(k[s]);
+        }
         refresh(K);
     }
 
