@@ -152,6 +152,20 @@ def test_f16_tiny_database_and_nq_one():
         assert_same(got_d, got_i, orc.adc_search_f16(centroids, d, codes, queries[:1], 10), "nq=1")
 
 
+@pytest.mark.parametrize("family", ["random", "tie"])
+def test_f16_single_query_over_many_blocks(family):
+    # one query spread over ~37 blocks: each block appends only its entries at or below the slab's published bound,
+    # and the last block merges those candidates; repeated searches check that the slab state starts fresh
+    gen = datagen.random_fixture if family == "random" else datagen.tie_fixture
+    n, d, m, nq = 300_007, 32, 16, 2
+    centroids, codes, queries = gen(n, d, m, nq, seed=41)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        for k in (1, 10, 64, 100, 10):
+            got_d, got_i, _ = s.search(queries[:1], k, F16)
+            assert s.last_launch().blocks_x > 8
+            assert_same(got_d, got_i, orc.adc_search_f16(centroids, d, codes, queries[:1], k), f"{family} k={k}")
+
+
 def test_f16_stays_close_to_the_fp32_path(fixture, searcher):
     # the recall delta: the fp16 tables change ranks only where fp32 distances are within table rounding
     centroids, codes, queries = fixture
