@@ -102,7 +102,7 @@ int vk_abi_version(void);
 
 /* gpu.hpp:25 variant_name (names as searcher.cu:123-136), e.g. "v8_fused_warp"; "unknown" when out of range. */
 const char* vk_variant_name(int variant);
-/* gpu.hpp:26 is_fused (searcher.cu:138-141): 1 for v4-v8, 0 otherwise. */
+/* gpu.hpp:26 is_fused (searcher.cu:138-141): 1 for v4-v9, 0 otherwise (v4 is rejected before launch). */
 int vk_is_fused(int variant);
 /* Whether a variant needs m % 16 == 0 (bench_main.cpp:184-187; searcher.cu:243-246). */
 int vk_needs_m16(int variant);

@@ -121,10 +121,10 @@ struct ScanArgs {
 };
 hipError_t launch_scan(int variant, const ScanArgs& a, int blocks_x, int nq, int threads, hipStream_t stream);
 
-// ---- fused scans with per-thread lists, v4-v7 (scan_thread.hip): grid (blocks_x, ceil(nq / Q)), 256 threads
+// ---- fused scans with per-thread lists, v5-v7 (scan_thread.hip): grid (blocks_x, ceil(nq / Q)), 256 threads
 struct ThreadScanArgs {
     const float* lut;         // [nq padded to a multiple of Q][m][256]; padded tables are zero
-    const uint8_t* codes_il;  // v4, v5
+    const uint8_t* codes_il;  // v5
     const uint4* codes_v;     // v6, v7
     int64_t n;
     int m;

@@ -100,8 +100,8 @@ inline bool bulk_scan(const Partition& p, int ilp) {
     return per_block * 64 * ilp < kBulkScanVectors;
 }
 
-// blocks_x of the unfused scans and v4 (searcher.cu:172-177): an override, else about 8 blocks per CU over the
-// whole grid, never fewer than 16 vectors per thread.
+// blocks_x of the unfused scans (searcher.cu:172-177, where the reference also sizes v4 with it): an override, else
+// about 8 blocks per CU over the whole grid, never fewer than 16 vectors per thread.
 inline int64_t blocks_x_fill(int64_t n, int64_t grid_y, int threads, int cus, int blocks_per_query) {
     if (blocks_per_query > 0) return blocks_per_query;
     const int64_t by_work = (n + int64_t{threads} * 16 - 1) / (int64_t{threads} * 16);
