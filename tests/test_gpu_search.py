@@ -121,6 +121,24 @@ def test_long_lists_merge_whole(family):
             s.set_tuning(vk.Tuning(queries_per_block=1))
 
 
+@pytest.mark.parametrize("family", ["random", "tie"])
+def test_single_query_final_merge_paths(family):
+    # One query over many blocks with one-register lists (k <= 64): the last block bounds the k-th best by the k-th
+    # smallest list head of each wave's 64 lists and merges only the pairs at or below it. Cases: k=10 over 100
+    # lists (a few dozen survivors, one sort); k=33 over 100 lists and k=64 over 30 (no wave has 64 heads, so every
+    # real pair survives: more than 64, streamed from LDS); k=64 over 40 (2560 pairs overflow the 16 KB of LDS: the
+    # merge of every list). Tie-heavy data checks that pairs equal to the bound and the id order survive the filter.
+    gen = datagen.random_fixture if family == "random" else datagen.tie_fixture
+    n, d, m, nq = 400_009, 32, 16, 2
+    centroids, codes, queries = gen(n, d, m, nq, seed=31)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        for k, bpq in ((10, 100), (33, 100), (64, 30), (64, 40), (1, 256)):
+            s.set_tuning(vk.Tuning(queries_per_block=1, blocks_per_query=bpq))
+            got_d, got_i, _ = s.search(queries[:1], k, vk.ScanVariant.FusedWarp)
+            assert s.last_launch().blocks_x == bpq
+            assert_same(got_d, got_i, orc.adc_search(centroids, d, codes, queries[:1], k), f"{family} k={k} bpq={bpq}")
+
+
 def test_bulk_and_one_by_one_admission_agree():
     # Blocks that scan few vectors of a slab use the instance admitting candidates in bulk; above 2^18 vectors per
     # block and slab the one admitting them one by one (the headline's). 300k vectors with one block per slab take

@@ -320,13 +320,104 @@ __device__ __forceinline__ void merge_query_wave(const Pair* first, int lists, i
     }
 }
 
+__device__ __forceinline__ uint64_t lane_read_key(uint64_t v, int lane) {
+    const uint32_t lo = static_cast<uint32_t>(lane_read(static_cast<int32_t>(static_cast<uint32_t>(v)), lane));
+    const uint32_t hi = static_cast<uint32_t>(lane_read(static_cast<int32_t>(static_cast<uint32_t>(v >> 32)), lane));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Final merge of one query over many partial lists of K <= 64 sorted pairs (`first[l * K + j]`) by a bound and a
+// filter instead of merge networks over every pair. Wave w sorts the heads (entry 0) of lists 64w .. 64w+63: when
+// K of them are real, their K-th smallest key T_w has K entries of distinct lists at or below it, so the query's
+// K-th best is at or below it too; T = min over the waves. Every pair above T, and every empty slot, is dropped;
+// the survivors (a few dozen for hundreds of lists) are appended to LDS, and wave 0 sorts them in one network (or,
+// more than 64, streams them through a wave list). The result is the K smallest pairs by (dist, id), the same as
+// a merge of every list. The pair loads are issued before the head sort, so their round trip overlaps it. LDS
+// `buf` holds the W bounds, the survivor count and the survivors (`buf_pairs` pairs in all); returns false, for
+// every thread, when the survivors do not fit (the caller then merges every list). Called by all threads.
+template <int W>
+__device__ bool merge_query_filtered(const Pair* first, int lists, int K, int k, Pair* out, int shift, Pair* buf,
+                                     int buf_pairs, int wave, int lane) {
+    uint64_t* const bounds = reinterpret_cast<uint64_t*>(buf);
+    unsigned* const count = reinterpret_cast<unsigned*>(buf + W);
+    Pair* const surv = buf + W + 1;
+    const int cap = buf_pairs - (W + 1);
+    const int64_t total = static_cast<int64_t>(lists) * K;
+    constexpr int B = 8;  // rounds of W * 64 pairs per batch, all loads of a batch in flight
+    constexpr int64_t kRound = static_cast<int64_t>(W) * WAVE;
+    Pair p[B];
+    auto load_batch = [&](int64_t base) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int64_t e = base + u * kRound + wave * WAVE + lane;
+            p[u] = e < total ? first[e] : Pair{INFINITY, kEmptyId};
+        }
+    };
+    uint64_t head = kEmptyKey;
+    const int hl = wave * WAVE + lane;
+    if (hl < lists) {
+        const Pair h = first[static_cast<int64_t>(hl) * K];
+        head = pair_key(h.d, h.i);
+    }
+    load_batch(0);
+    wave_sort<2, false>(head);
+    if (lane == 0) bounds[wave] = lane_read_key(head, K - 1);
+    if (wave == 0 && lane == 0) *count = 0u;
+    __syncthreads();
+    uint64_t t = bounds[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) t = bounds[w] < t ? bounds[w] : t;
+    for (int64_t base = 0; base < total; base += B * kRound) {
+        if (base > 0) load_batch(base);
+        uint64_t keep[B];
+        unsigned n = 0;
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            keep[u] = __builtin_amdgcn_ballot_w64(p[u].i != kEmptyId && pair_key(p[u].d, p[u].i) <= t);
+            n += static_cast<unsigned>(__popcll(keep[u]));
+        }
+        if (n == 0) continue;  // wave-uniform
+        unsigned at = 0;
+        if (lane == 0) at = atomicAdd(count, n);
+        at = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(at)));
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const unsigned pos = at + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(keep[u] >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(keep[u]), 0u));
+            if (((keep[u] >> lane) & 1) && pos < static_cast<unsigned>(cap)) surv[pos] = p[u];
+            at += static_cast<unsigned>(__popcll(keep[u]));
+        }
+    }
+    __syncthreads();
+    const unsigned survivors = *count;
+    if (survivors > static_cast<unsigned>(cap)) return false;  // block-uniform: every thread read the same count
+    if (wave == 0) {
+        if (survivors <= static_cast<unsigned>(WAVE)) {
+            uint64_t key = kEmptyKey;
+            if (static_cast<unsigned>(lane) < survivors) key = pair_key(surv[lane].d, surv[lane].i);
+            wave_sort<2, false>(key);
+            if (lane < k) out[lane] = final_pair(key_dist(key), key_id(key), shift);
+        } else {
+            WaveList<1, true> wl;
+            wl.init();
+            stream_pairs(wl, surv, 0, 4 * WAVE, static_cast<int>(survivors), K, lane);
+            if (lane < k) out[lane] = final_pair(wl.d[0], wl.id[0], shift);
+        }
+    }
+    __syncthreads();
+    return true;
+}
+
 // Final merge of one query of a slab by the last block to finish the slab: the slab's `lists` partial lists for
-// the query (K pairs each, `first[l * K + j]`) are split over the W waves, each streaming its share through a wave
-// list; wave 0 then streams the W wave lists (LDS `buf`, W * K pairs) into the query's k results. Called by all
-// threads of the block.
+// the query (K pairs each, `first[l * K + j]`); for K <= 64 by the filter above when its survivors fit in `buf`.
+// Otherwise they are split over the W waves, each streaming its share through a wave list; wave 0 then streams the
+// W wave lists (LDS `buf`, W * K pairs) into the query's k results. Called by all threads of the block.
 template <int S, int W>
 __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K, int k, Pair* out, int shift,
-                                            Pair* buf, int wave, int lane) {
+                                            Pair* buf, int buf_pairs, int wave, int lane) {
+    if constexpr (S == 1) {
+        if (merge_query_filtered<W>(first, lists, K, k, out, shift, buf, buf_pairs, wave, lane)) return;
+    }
     WaveList<S, true> wl;
     wl.init();
     stream_partials(wl, first, wave, W, lists, K, lane);
@@ -436,12 +527,14 @@ __global__ void __launch_bounds__(T)
     float published[QS];
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
     int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
-    // One query per block over 16-byte codes: the next granule's code words are loaded before this granule's
-    // lookups (U more registers), so a wave's next memory round trip overlaps its own lookups; a slab's first
-    // granule is loaded before the tables are built. With one query per block the codes stream from HBM and the
-    // few waves per CU leave that latency open otherwise; the multi-query instances read codes mostly from L2 and
-    // need the registers for their accumulators.
-    constexpr bool kPrefetch = !IVF && QS == 1 && M == 16;
+    // One or four queries per block over 16-byte codes: the next granule's code words are loaded before this
+    // granule's lookups (U more registers), so a wave's next memory round trip overlaps its own lookups; a slab's
+    // first granule is loaded before the tables are built. With one query per block the codes stream from HBM and
+    // the few waves per CU leave that latency open otherwise. Four queries, where an even partition spreads the
+    // blocks over the codes so that most code reads miss the L2s: 10M x nq=1000 -0.3 %, 100M -0.9 %, 1M unchanged
+    // (16 more VGPRs; the kernel's spills grow, outside the scan loop). Two queries read codes mostly from L2; the
+    // fp16 eight-query kernel has no registers for it.
+    constexpr bool kPrefetch = !IVF && M == 16 && (QS == 1 || (!F16 && QG == 4 && NG == 1));
     uint4 next_words[kPrefetch ? U : 1];
 
     for (int64_t item = start; item < end;) {
@@ -752,7 +845,7 @@ __global__ void __launch_bounds__(T)
                                         a.k, a.out + (slab * QS + q) * a.k, F16 ? table_shift(qmax[q]) : 0, lane);
             } else if (slab < static_cast<int64_t>(a.nq)) {  // one query (Q = 1) over many blocks: all waves
                 merge_query<S, W>(slab_part, count, a.K, a.k, a.out + slab * a.k, F16 ? table_shift(qmax[0]) : 0,
-                                  buf, wave, lane);
+                                  buf, NG * table_bytes / static_cast<int>(sizeof(Pair)), wave, lane);
             }
         }
         item = slab_next;
