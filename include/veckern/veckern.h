@@ -157,7 +157,7 @@ int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq, size_t k
  * VK_NOALLOC_COUNTER_BYTES for the counters, one 4-byte counter per slab of queries_per_block queries; the rest for
  * the partial lists), so the call makes no device allocation, creates no events and records no timings. A search
  * needing more than that (very large nq x k) is rejected before any launch with VK_ERR_INVALID_ARGUMENT; split it
- * into smaller calls. The searcher's word-interleaved code layout must already exist: one vk_search or
+ * into smaller calls. The searcher's sorted code layout (v8 and v9) must already exist: one vk_search or
  * vk_search_device call with v8 or v9 builds it (that call allocates); otherwise VK_ERR_LOGIC. Calls on one device
  * share its array: the library serialises them within a process (a per-device lock held until the call's stream
  * has finished), and overlapping calls would otherwise race on it. Synchronous, like vk_search_device. */

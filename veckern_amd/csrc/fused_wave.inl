@@ -427,6 +427,27 @@ __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K,
     __syncthreads();
 }
 
+// Vector ids of a granule's U tiles in the sorted code layout (exhaustive scans): per slot, the index of its vector
+// within the slot's run of 65536 slots, 16 bits, interleaved by four tiles ([tile / 4][lane][tile % 4]), so one
+// load of 2U bytes gives a lane the ids of its U tiles (a granule's tiles start at a multiple of U, and U <= 4).
+template <int U>
+struct SlotIds {
+    uint32_t w[U == 4 ? 2 : 1];
+    __device__ __forceinline__ void load(const uint16_t* slot_ids, int64_t tile0, int lane) {
+        const uint16_t* p = slot_ids + (tile0 >> 2) * 256 + lane * 4 + (tile0 & 3);
+        if constexpr (U == 4) {
+            const uint2 v = *reinterpret_cast<const uint2*>(p);
+            w[0] = v.x;
+            w[1] = v.y;
+        } else if constexpr (U == 2) {
+            w[0] = *reinterpret_cast<const uint32_t*>(p);
+        } else {
+            w[0] = *p;
+        }
+    }
+    __device__ __forceinline__ uint32_t get(int u) const { return (w[u >> 1] >> (16 * (u & 1))) & 0xffffu; }
+};
+
 // QG: queries per table (1, 2, 4; 8 with fp16 entries). NG: tables per block (1, 2). U: 64-vector tiles per wave
 // step. M: sub-spaces if fixed at compile time, 0 for any m % 16 == 0. S: list registers per lane (K <= 64 * S).
 // F16: binary16 table entries.
@@ -536,6 +557,7 @@ __global__ void __launch_bounds__(T)
     // fp16 eight-query kernel has no registers for it.
     constexpr bool kPrefetch = !IVF && M == 16 && (QS == 1 || (!F16 && QG == 4 && NG == 1));
     uint4 next_words[kPrefetch ? U : 1];
+    SlotIds<U> next_ids;
 
     for (int64_t item = start; item < end;) {
         // The slab holding `item` and its granules [slab_first, slab_next) in the balanced partition.
@@ -585,6 +607,7 @@ __global__ void __launch_bounds__(T)
                 const uint4* c = a.codes + (g_lo + wave) * U * WAVE + lane;
 #pragma unroll
                 for (int u = 0; u < U; ++u) next_words[u] = c[u * WAVE];
+                next_ids.load(a.slot_ids, (g_lo + wave) * U, lane);
             }
         }
 
@@ -645,20 +668,26 @@ __global__ void __launch_bounds__(T)
             // count within what the LDS-limited residency allows.
             constexpr int WORDS = M ? M / 16 : 1;
             uint4 cw[U][WORDS];
+            SlotIds<U> ids;
             if constexpr (kPrefetch) {
                 const int64_t g_next = g_lo + static_cast<int64_t>(__builtin_amdgcn_readfirstlane(grab));
 #pragma unroll
                 for (int u = 0; u < U; ++u) cw[u][0] = next_words[u];
+                ids = next_ids;
                 if (g_next < g_hi) {
                     const uint4* c = a.codes + g_next * U * WAVE + lane;
 #pragma unroll
                     for (int u = 0; u < U; ++u) next_words[u] = c[u * WAVE];
+                    next_ids.load(a.slot_ids, g_next * U, lane);
                 }
-            } else if constexpr (M > 0) {
+            } else {
+                if constexpr (M > 0) {
 #pragma unroll
-                for (int u = 0; u < U; ++u)
+                    for (int u = 0; u < U; ++u)
 #pragma unroll
-                    for (int w = 0; w < WORDS; ++w) cw[u][w] = tile_codes[(u * WORDS + w) * WAVE];
+                        for (int w = 0; w < WORDS; ++w) cw[u][w] = tile_codes[(u * WORDS + w) * WAVE];
+                }
+                if constexpr (!IVF) ids.load(a.slot_ids, tile0, lane);
             }
             // Inverted lists: the tiles' vector ids travel with their codes (loaded after a tile's lookups, each
             // would cost its own memory round trip behind the scheduling fence).
@@ -740,9 +769,12 @@ __global__ void __launch_bounds__(T)
                     id = static_cast<uint32_t>(vid);
                     valid = __builtin_amdgcn_ballot_w64(vid >= 0);
                 } else {
+                    // Slots [0, n) hold real vectors in every run of the sorted layout; the id is the run's first
+                    // slot plus the vector's index within the run.
                     const uint32_t first = static_cast<uint32_t>((tile0 + u) * WAVE);
-                    id = first + static_cast<uint32_t>(lane);
-                    valid = first + WAVE <= n32 ? ~uint64_t{0} : __builtin_amdgcn_ballot_w64(id < n32);
+                    id = ((first >> 16) << 16) + ids.get(u);
+                    valid = first + WAVE <= n32 ? ~uint64_t{0}
+                                                : __builtin_amdgcn_ballot_w64(first + static_cast<uint32_t>(lane) < n32);
                 }
 #pragma unroll
                 for (int q = 0; q < QS; ++q) {

@@ -15,9 +15,11 @@ inline int dispatched_k(size_t k) {
     return 0;
 }
 
-// v3-v5 read the byte-interleaved layout, v6-v8 the 16-byte-word one (searcher.cu:222-241).
+// v3-v5 read the byte-interleaved layout, v6-v7 the 16-byte-word one (searcher.cu:222-241); v8 and v9 read the
+// same words with the vectors in a sorted slot order.
 inline bool uses_byte_layout(int v) { return v == 3 || v == 4 || v == 5; }
-inline bool uses_word_layout(int v) { return v == 6 || v == 7 || v == 8 || v == 9; }
+inline bool uses_word_layout(int v) { return v == 6 || v == 7; }
+inline bool uses_sorted_layout(int v) { return v == 8 || v == 9; }  // words in the fused scans' slot order
 
 // Queries per block: the requested Q, halved until the Q tables (Q * m * 256 entries) fit in LDS; for per-thread
 // lists (v7) also until Q * K <= 64, as searcher.cu:213-220. entry_bytes: 4 for fp32 tables, 2 for fp16.
