@@ -87,14 +87,6 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
     // slabs no more than the slots: floor(slots / slabs) whole blocks per slab (1M x nq=1000 at Q = 4: 2 each)
     const Partition b = balanced_partition(1'000'000, 1000, 4, 4, 512, 0, 256);
     EXPECT(b.grid == 500 && b.max_slots == 2);
-    // `even`: at most kEvenMaxPerSlab blocks per slab that leave slots idle give way to the even partition over all
-    // slots (the 1M headline: 512 blocks, a slab's granules over at most 4 of them)
-    const Partition e = balanced_partition(1'000'000, 1000, 4, 4, 512, 0, 256, true);
-    EXPECT(e.grid == 512 && e.max_slots <= 4);
-    EXPECT(balanced_partition(1'000'000, 1000, 4, 4, 500, 0, 256, true).grid == 500);   // no slot idle: aligned
-    EXPECT(balanced_partition(1'000'000, 1000, 8, 4, 512, 0, 256, true).grid == 500);   // 4 per slab: aligned
-    EXPECT(balanced_partition(10'000'000, 1, 1, 4, 512, 0, 256, true).grid == 256);     // capped by the CUs
-    EXPECT(balanced_partition(100'000, 100, 4, 4, 512, 0, 256, true).grid == 25 * 13);  // capped by n
     EXPECT(balanced_partition(1'000'000, 1000, 4, 4, 256, 0, 256).grid == 250);  // one block per slab
     EXPECT(balanced_partition(1'000'000, 1000, 2, 4, 256, 0, 256).grid == 256);  // 500 slabs > 256 slots
     // small slabs: at most ceil(n / kMinBlockVectors) blocks each (100k vectors: 13 blocks of ~7.7k vectors)
@@ -111,16 +103,13 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
         const int64_t slots = 1 + static_cast<int64_t>(rng() % 1100);
         const int bpq = (trial % 3 == 0) ? static_cast<int>(1 + rng() % 40) : 0;
         const int64_t cus = (trial % 2 == 0) ? 1 + static_cast<int64_t>(rng() % 300) : 0;
-        const bool even = trial % 5 == 1;
-        const Partition p = balanced_partition(n, nq, q, ilp, slots, bpq, cus, even);
+        const Partition p = balanced_partition(n, nq, q, ilp, slots, bpq, cus);
         EXPECT(p.slabs == static_cast<int64_t>((nq + q - 1) / q));
         EXPECT(p.n_gran == ((n + 63) / 64 + ilp - 1) / ilp);
         EXPECT(p.total == p.slabs * p.n_gran && p.grid >= 1 && p.grid <= p.total);
         if (bpq == 0) EXPECT(p.grid <= slots);
         if (bpq == 0 && cus > 0) EXPECT(p.grid <= p.slabs * cus);  // a slab never gets more blocks than CUs
-        // whole blocks per slab (no block crosses a boundary), unless the even partition was taken
-        const bool aligned = bpq > 0 || (p.slabs <= slots && !(even && p.grid % p.slabs != 0));
-        if (even && bpq == 0 && p.slabs <= slots && p.grid % p.slabs != 0) EXPECT(p.grid == std::min(slots, p.total));
+        const bool aligned = bpq > 0 || p.slabs <= slots;  // whole blocks per slab: no block crosses a boundary
         if (aligned) EXPECT(p.grid % p.slabs == 0);
         // block ranges tile [0, total) in order, and every block is non-empty
         int64_t prev_end = 0;

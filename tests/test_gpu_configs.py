@@ -105,14 +105,11 @@ def test_config_b_headline_all_queries_and_launch_shape():
     w, shape = run_config("B", 4, 1000)
     info = vk.device_info()
     assert shape.threads == 512 and shape.queries_per_block == 4 and shape.vectors_per_step == 4
-    # 250 slabs of 4 queries; with R resident blocks (occupancy x CUs) every slab gets floor(R / 250) of them, unless
-    # that is at most 2 and leaves slots idle: then the even partition over all R slots (blocks cross slabs).
+    # 250 slabs of 4 queries; with R resident blocks (occupancy x CUs) every slab gets floor(R / 250) of them.
     resident = shape.blocks_per_sm * info.sm_count
-    per_slab = resident // 250
-    even = per_slab <= 2 and 250 * per_slab < resident
-    assert shape.blocks_x == (resident if even else 250 * per_slab), (shape.blocks_x, resident)
+    assert shape.blocks_x == 250 * (resident // 250), (shape.blocks_x, resident)
     if info.sm_count == 256 and shape.blocks_per_sm == 2:
-        assert shape.blocks_x == 512
+        assert shape.blocks_x == 500
 
 
 @pytest.mark.parametrize("cfg,q", [("C32", 4), ("C64", 2)])

@@ -371,7 +371,7 @@ struct vk_searcher {
 
         w.part = vk::plan::balanced_partition(static_cast<int64_t>(n), b, w.q, w.ilp,
                                               static_cast<int64_t>(w.per_cu) * info.sm_count,
-                                              tuning.blocks_per_query, info.sm_count, !f16 && segments == 1);
+                                              tuning.blocks_per_query, info.sm_count);
         // Few vectors per block: the instance that admits candidates in bulk, if it has the same residency (the
         // partition above was planned with it).
         if (!f16 && segments == 1 && w.q > 1 && vk::plan::bulk_scan(w.part, w.ilp)) {

@@ -548,14 +548,13 @@ __global__ void __launch_bounds__(T)
     float published[QS];
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
     int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
-    // One or four queries per block over 16-byte codes: the next granule's code words are loaded before this
+    // One query per block over 16-byte codes: the next granule's code words and ids are loaded before this
     // granule's lookups (U more registers), so a wave's next memory round trip overlaps its own lookups; a slab's
-    // first granule is loaded before the tables are built. With one query per block the codes stream from HBM and
-    // the few waves per CU leave that latency open otherwise. Four queries, where an even partition spreads the
-    // blocks over the codes so that most code reads miss the L2s: 10M x nq=1000 -0.3 %, 100M -0.9 %, 1M unchanged
-    // (16 more VGPRs; the kernel's spills grow, outside the scan loop). Two queries read codes mostly from L2; the
-    // fp16 eight-query kernel has no registers for it.
-    constexpr bool kPrefetch = !IVF && M == 16 && (QS == 1 || (!F16 && QG == 4 && NG == 1));
+    // first granule is loaded before the tables are built. With one query per block the codes stream from HBM and the
+    // few waves per CU leave that latency open otherwise. The multi-query instances read codes mostly from L2 and
+    // need the registers for their accumulators (four queries, sorted codes, slab-aligned blocks: 1M x nq=1000
+    // +4.5 % with the prefetch, 10M +3.6 %).
+    constexpr bool kPrefetch = !IVF && QS == 1 && M == 16;
     uint4 next_words[kPrefetch ? U : 1];
     SlotIds<U> next_ids;
 

@@ -45,28 +45,19 @@ inline int64_t first_block(int64_t item, int64_t grid, int64_t total) { return (
 // the slabs*n_gran items are split evenly over `grid` blocks. blocks_per_query > 0 fixes the blocks per slab.
 // Otherwise, when the slabs are no more than the resident blocks (`slots`), each slab gets floor(slots / slabs)
 // blocks, at most `cus` (> 0) of them and at most ceil(n / kMinBlockVectors), so that no block crosses a
-// slab boundary (unless `even` and that leaves slots idle, see kEvenMaxPerSlab); with more slabs than slots, grid =
-// slots and blocks span slab boundaries. Measured on MI355X: in the first form of the scan (granules assigned
-// statically to waves), blocks crossing slabs made the two blocks sharing a CU finish ~0.4 ms apart at 1M x
-// nq=1000 (the older block's waves get issue priority): 1.43 ms against 1.35 ms slab-aligned (fp16 tables at Q = 8:
-// 1.07 -> 0.90 ms), hence the aligned layout; with granules handed out per block it still wins wherever it leaves
-// few slots idle. A slab's blocks beyond one per CU only lengthen its final merge (nq = 1 at 10M: 73 -> 67 us).
+// slab boundary; with more slabs than slots, grid = slots and blocks span slab boundaries. Measured on MI355X: with
+// granules assigned statically to waves, blocks crossing slabs made the two blocks sharing a CU finish ~0.4 ms apart
+// at 1M x nq=1000 (the older block's waves get issue priority): 1.43 ms against 1.35 ms slab-aligned (fp16 tables at
+// Q = 8: 1.07 -> 0.90 ms). Aligned blocks also sweep the codes in lockstep (the blocks on each part of the codes read
+// the same lines at about the same time, so the L2s serve most code reads). An even split over every resident slot
+// when the aligned layout leaves slots idle (250 slabs on 512 slots) gained 0.5-1.6 % with codes in vector order,
+// but on the sorted code layout, where the scan is faster and leans on the L2s, it lost: 1M x nq=1000 +7.7 %, 10M
+// +9.6 %, 100M +1.5 %. A slab's blocks beyond one per CU only lengthen its final merge (nq = 1 at 10M: 73 -> 67 us).
 // kMinBlockVectors: 16 vectors per thread of a 512-thread block, the reference's rule for how far a search is spread
 // (searcher.cu:196-197; its tests/test_gpu.cpp:139-145 expect a single query over at least ceil(n / (16 * threads))
 // blocks). Fewer vectors per block and a block's table build and merges outweigh its scan (100k vectors, nq=100:
 // 20 blocks per slab 94 us, 10 blocks 78 us).
 constexpr int64_t kMinBlockVectors = 8192;
-
-// With at most kEvenMaxPerSlab blocks per slab left to the aligned layout, its rounding leaves resident slots idle
-// (250 slabs on 512 slots: 12 CUs hold one block and idle half the search); `even` then takes the even partition
-// over every slot, with blocks crossing slab boundaries. Measured for one-register fp32 lists (kernel time, nq=1000):
-// Q = 4 at 1M -0.5 to -1 %, 10M -1.6 %, 100M -1.3 %; Q = 2 at 1M -0.3 %, 10M -1.2 %, 100M +0.4 %. The price is
-// L2 locality: aligned blocks of every slab move through the same code lines together, even ones start at spread
-// offsets, so the L2s miss on most code reads (1M, Q = 4: 0.13 -> 3.7 GB per launch from the memory side); the
-// 256 MB MALL serves them at 1M and 10M, and at 100M and Q = 2 the code stream (~6 TB/s) meets HBM's limit. Not for
-// two-register lists (1M m32 k=100 +2.2 %: a crossing block restarts four 100-entry lists) nor fp16 tables at four
-// blocks per slab (+7.6 %).
-constexpr int64_t kEvenMaxPerSlab = 2;
 
 struct Partition {
     int64_t slabs = 0, n_gran = 0, total = 0, grid = 0;
@@ -74,7 +65,7 @@ struct Partition {
 };
 
 inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_t slots, int blocks_per_query,
-                                    int64_t cus = 0, bool even = false) {
+                                    int64_t cus = 0) {
     Partition p;
     p.slabs = static_cast<int64_t>((nq + q - 1) / q);
     const int64_t tiles = (n + 63) / 64;
@@ -84,10 +75,8 @@ inline Partition balanced_partition(int64_t n, size_t nq, int q, int ilp, int64_
     int64_t per_slab = blocks_per_query;
     if (per_slab <= 0 && p.slabs <= slots) {
         per_slab = slots / p.slabs;
-        const int64_t by_slots = per_slab;
         if (cus > 0) per_slab = std::min(per_slab, cus);
         per_slab = std::max<int64_t>(1, std::min(per_slab, (n + kMinBlockVectors - 1) / kMinBlockVectors));
-        if (even && per_slab == by_slots && per_slab <= kEvenMaxPerSlab && p.slabs * per_slab < slots) per_slab = 0;
     }
     if (per_slab > 0)
         p.grid = p.slabs * std::min<int64_t>(per_slab, p.n_gran);
