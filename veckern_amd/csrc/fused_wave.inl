@@ -60,6 +60,41 @@ struct Entries {
         std::conditional_t<QG == 1, uint16_t,
                            std::conditional_t<QG == 2, uint32_t, std::conditional_t<QG == 4, uint2, uint4>>>,
         std::conditional_t<QG == 1, float, std::conditional_t<QG == 2, float2, float4>>>;
+    // The first sub-space's entries: acc = entry equals the reference's 0.f + entry bit for bit, since entries
+    // are sums of squares (+0 or above, never -0), and saves the zeroing and one add per query and vector.
+    __device__ static void set(float* acc, const T& v) {
+        if constexpr (!F16) {
+            if constexpr (QG == 1) {
+                acc[0] = v;
+            } else if constexpr (QG == 2) {
+                acc[0] = v.x;
+                acc[1] = v.y;
+            } else {
+                acc[0] = v.x;
+                acc[1] = v.y;
+                acc[2] = v.z;
+                acc[3] = v.w;
+            }
+        } else {
+            auto widen = [&](int i, uint32_t h2) {  // the exact fp32 values of a pair of binary16 entries
+                acc[i] = static_cast<float>(__builtin_bit_cast(half2_t, h2).x);
+                acc[i + 1] = static_cast<float>(__builtin_bit_cast(half2_t, h2).y);
+            };
+            if constexpr (QG == 1) {
+                acc[0] = static_cast<float>(__builtin_bit_cast(_Float16, v));
+            } else if constexpr (QG == 2) {
+                widen(0, v);
+            } else if constexpr (QG == 4) {
+                widen(0, v.x);
+                widen(2, v.y);
+            } else {
+                widen(0, v.x);
+                widen(2, v.y);
+                widen(4, v.z);
+                widen(6, v.w);
+            }
+        }
+    }
     __device__ static void add(float* acc, const T& v, _Float16 one) {
         if constexpr (!F16) {
             if constexpr (QG == 1) {
@@ -118,6 +153,21 @@ __device__ __forceinline__ int table_shift(uint32_t max_bits) {
 __device__ __forceinline__ uint32_t to_half_bits(float x) {  // round to nearest even
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
+
+// Byte b of w times 2^SHIFT (a table entry's byte offset) in one VALU op: the compiler selects a shift with an SDWA
+// byte select for bytes 1-3 by itself, but turns byte 0 into a shift and a mask; the asm keeps byte 0 to one op as
+// well (the shift amount sits in a VGPR, as SDWA requires).
+template <int SHIFT>
+__device__ __forceinline__ uint32_t scaled_byte(uint32_t w, int b) {
+    if (b != 0) return ((w >> (8 * b)) & 0xffu) << SHIFT;
+    uint32_t r;
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r)
+        : "v"(static_cast<uint32_t>(SHIFT)), "v"(w));
+    return r;
+}
+
+constexpr int log2_int(int x) { return x <= 1 ? 0 : 1 + log2_int(x / 2); }
 
 // Loads n consecutive floats from p (16-byte aligned when n % 4 == 0, 8-byte aligned when n == 2) with the widest
 // vector loads the alignment allows.
@@ -698,11 +748,16 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 float acc[QS];
+                if constexpr (M == 0) {
 #pragma unroll
-                for (int q = 0; q < QS; ++q) acc[q] = 0.f;
-                // 16 lookups of one code word, sub-spaces 16w .. 16w+15 in order.
+                    for (int q = 0; q < QS; ++q) acc[q] = 0.f;
+                }
+                // 16 lookups of one code word, sub-spaces 16w .. 16w+15 in order; the first sub-space of a vector
+                // (w == 0 with m fixed) sets the accumulators instead of adding to zeroed ones.
+                constexpr int kShift = log2_int(E::kBytes);
                 auto lookup_word = [&](const uint4 word, const int w) {
                     const uint32_t part[4] = {word.x, word.y, word.z, word.w};
+                    const bool first = M > 0 && w == 0;
                     if constexpr (F16 && QG >= 4) {
                         // The word's reads are issued eight at a time before their accumulations: the
                         // one-statement-per-read accumulations would otherwise be scheduled right behind their own
@@ -715,30 +770,34 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
                             for (int jj = 0; jj < 8; ++jj) {
                                 const int j = h * 8 + jj;
-                                const uint32_t c = (part[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                                const uint32_t off = scaled_byte<kShift>(part[j >> 2], j & 3);
                                 const int s = w * 16 + j;
 #pragma unroll
                                 for (int t = 0; t < NG; ++t)
                                     v[jj * NG + t] = *reinterpret_cast<const V*>(
-                                        tables + t * table_bytes + (s * KSUB + static_cast<int>(c)) * E::kBytes);
+                                        tables + t * table_bytes + s * KSUB * E::kBytes + off);
                             }
                             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                             for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-                                for (int t = 0; t < NG; ++t) E::add(&acc[t * QG], v[jj * NG + t], one);
+                                for (int t = 0; t < NG; ++t) {
+                                    if (first && h == 0 && jj == 0) E::set(&acc[t * QG], v[jj * NG + t]);
+                                    else E::add(&acc[t * QG], v[jj * NG + t], one);
+                                }
                         }
                         return;
                     }
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
-                        const uint32_t c = (part[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                        const uint32_t off = scaled_byte<kShift>(part[j >> 2], j & 3);
                         const int s = w * 16 + j;
 #pragma unroll
                         for (int t = 0; t < NG; ++t) {
-                            const V v = *reinterpret_cast<const V*>(tables + t * table_bytes +
-                                                                    (s * KSUB + static_cast<int>(c)) * E::kBytes);
-                            E::add(&acc[t * QG], v, one);
+                            const V v = *reinterpret_cast<const V*>(tables + t * table_bytes + s * KSUB * E::kBytes +
+                                                                    off);
+                            if (first && j == 0) E::set(&acc[t * QG], v);
+                            else E::add(&acc[t * QG], v, one);
                         }
                     }
                 };
