@@ -2,6 +2,9 @@
 //   - vkb_lds_floor: uniform random byte-indexed lookups into query-interleaved LDS tables, the same table
 //     layout ([s][c][QG] floats), block size and LDS footprint as the fused scan, codes generated in registers
 //     (no global loads). Its lookups/s is the LDS-lookup roofline the scan is measured against.
+//   - vkb_lds_peak: the same 16-byte table reads with no bank conflict (each 16-lane pass of a wave64 ds_read_b128
+//     touches 16 distinct 16-byte bank groups) and almost no VALU work: the LDS's own read rate, against which the
+//     scan's 64-lookups-per-CU-cycle peak (256 B/clk/CU) is checked.
 //   - vkb_hbm_read: 16-byte streaming reads of a large buffer (the HBM read roofline).
 //   - vkb_copy: a plain copy of known size, run under rocprofv3 to calibrate FETCH_SIZE / WRITE_SIZE.
 #include <hip/hip_runtime.h>
@@ -65,6 +68,30 @@ __global__ void __launch_bounds__(kThreads) lds_floor_kernel(float* out, int ite
         for (int k = 0; k < 4; ++k) w[k] = __builtin_amdgcn_alignbit(w[k], w[k], 7) ^ static_cast<uint32_t>(it);
     }
     out[gid] = acc;
+}
+
+// Conflict-free 16-byte reads: lane l of every 16-lane pass reads bank group (l + s) % 16 of sub-space s; the
+// addresses are held in registers and each read's four floats are kept live by an empty asm (no adds).
+__global__ void __launch_bounds__(kThreads) lds_peak_kernel(float* out, int iters) {
+    __shared__ __align__(16) float table[kM * 256 * 4];
+    for (int j = threadIdx.x; j < kM * 256 * 4; j += kThreads) table[j] = static_cast<float>(j & 1023) * 1e-3f;
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t addr[kM];
+#pragma unroll
+    for (int s = 0; s < kM; ++s) addr[s] = (s * 256u + (((lane + s) & 15u) | ((lane >> 4) << 4))) * 16u;
+    float acc = 0.f;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int s = 0; s < kM; ++s) {
+            uint32_t a = addr[s];
+            asm volatile("" : "+v"(a));
+            const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(table) + a);
+            asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+            if (s == 0) acc += v.x;
+        }
+    }
+    out[blockIdx.x * kThreads + threadIdx.x] = acc;
 }
 
 __global__ void __launch_bounds__(256) hbm_read_kernel(const uint4* __restrict__ p, size_t n16, uint32_t* out) {
@@ -140,6 +167,27 @@ VKB_EXPORT int vkb_lds_floor(int qg, int iters, int reps, double* lookups_per_s,
 }
 
 // Streaming read bandwidth over `bytes` (a multiple of 16), best of reps, in GB/s.
+// Conflict-free LDS read rate in 4-byte table entries per second (four per lane per ds_read_b128). 0 on success.
+VKB_EXPORT int vkb_lds_peak(int iters, int reps, double* entries_per_s) {
+    const int cus = cu_count();
+    if (cus <= 0 || iters <= 0 || reps <= 0) return 1;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&lds_peak_kernel), kThreads,
+                                                     0) != hipSuccess || per_cu < 1)
+        return 1;
+    const int grid = cus * per_cu;
+    float* out = nullptr;
+    if (hipMalloc(&out, static_cast<size_t>(grid) * kThreads * sizeof(float)) != hipSuccess) return 1;
+    float best = 0.f;
+    const int rc = time_best(reps, &best, [&] {
+        hipLaunchKernelGGL(lds_peak_kernel, dim3(grid), dim3(kThreads), 0, 0, out, iters);
+    });
+    (void)hipFree(out);
+    if (rc) return rc;
+    *entries_per_s = static_cast<double>(grid) * kThreads * iters * kM * 4 / (best * 1e-3);
+    return 0;
+}
+
 VKB_EXPORT int vkb_hbm_read(size_t bytes, int reps, double* gbs) {
     const int cus = cu_count();
     if (cus <= 0 || bytes < 16 || reps <= 0) return 1;
