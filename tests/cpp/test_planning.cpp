@@ -1,12 +1,17 @@
 // Host-side launch planning (veckern_amd/csrc/planning.hpp), on the CPU: list-length dispatch, Q capping, the
-// balanced work partition of the wave-list scan, and the blocks_x models of the grid kernels. The blocks_x model
+// balanced work partition of the wave-list scan, and the blocks_x models of the grid kernels; and the slot order of
+// the fused scans' code layout (veckern_amd/csrc/slot_order.hpp). The blocks_x model
 // is checked against launch shapes the reference recorded on an A100 (108 SMs, 4 resident blocks per SM).
+#include <algorithm>
 #include <cstdint>
+#include <cstdio>
 #include <random>
+#include <utility>
 #include <vector>
 
 #include "check.hpp"
 #include "planning.hpp"
+#include "slot_order.hpp"
 
 using namespace vk::plan;
 
@@ -131,3 +136,84 @@ CASE("balanced_partition covers every item exactly once and bounds the slots per
 }
 
 int main() { return vktest::run(); }
+
+namespace {
+
+std::vector<uint8_t> random_codes(size_t n, size_t m, uint64_t seed, int distinct_rows = 0) {
+    std::mt19937_64 rng(seed);
+    std::vector<uint8_t> c(n * m);
+    if (distinct_rows > 0) {  // clustered: every row one of a few prototypes
+        std::vector<uint8_t> proto(static_cast<size_t>(distinct_rows) * m);
+        for (auto& x : proto) x = static_cast<uint8_t>(rng());
+        for (size_t i = 0; i < n; ++i) {
+            const size_t r = rng() % distinct_rows;
+            std::copy(proto.begin() + r * m, proto.begin() + (r + 1) * m, c.begin() + i * m);
+        }
+    } else {
+        for (auto& x : c) x = static_cast<uint8_t>(rng());
+    }
+    return c;
+}
+
+// Mean over the full 256-slot blocks' (pass, sub-space) pairs of the largest number of distinct table entries in
+// one 16-byte bank group (entry % 16) among a pass's 16 lanes; vec_of(slot) gives the slot's vector.
+template <typename F>
+double bank_load(const std::vector<uint8_t>& codes, size_t n, size_t m, F vec_of) {
+    double total = 0;
+    size_t count = 0;
+    for (size_t p0 = 0; p0 + 16 <= n / 256 * 256; p0 += 16)
+        for (size_t s = 0; s < m; ++s) {
+            bool seen[256] = {};
+            int groups[16] = {}, mx = 0;
+            for (size_t l = 0; l < 16; ++l) {
+                const int e = codes[vec_of(p0 + l) * m + s];
+                if (seen[e]) continue;
+                seen[e] = true;
+                mx = std::max(mx, ++groups[e & 15]);
+            }
+            total += mx;
+            ++count;
+        }
+    return total / count;
+}
+
+}  // namespace
+
+CASE("slot order: each run's slots hold every one of its vectors once; padding holds 0; threads agree") {
+    const std::pair<size_t, size_t> shapes[] = {{1, 16},      {63, 16},    {300, 16},          {4096, 32},
+                                                {65536, 16},  {65536 + 700, 16}, {3 * 65536 + 17, 16}};
+    for (const auto& [n, m] : shapes)
+        for (int clustered : {0, 5}) {
+            const std::vector<uint8_t> codes = random_codes(n, m, n * 7 + m + clustered, clustered);
+            const size_t n_pad = (n + 255) / 256 * 256;
+            const std::vector<uint16_t> ids = vk::order::slot_ids(codes.data(), n, m, n_pad, 1);
+            EXPECT(ids == vk::order::slot_ids(codes.data(), n, m, n_pad, 3));
+            EXPECT(ids.size() == n_pad);
+            for (size_t r0 = 0; r0 < n; r0 += vk::order::kRun) {
+                const size_t len = std::min(vk::order::kRun, n - r0);
+                std::vector<char> seen(len, 0);
+                bool ok = true;
+                for (size_t slot = r0; slot < r0 + len; ++slot) {
+                    const size_t v = ids[vk::order::interleaved(slot)];
+                    ok = ok && v < len && !seen[v];
+                    if (v < len) seen[v] = 1;
+                }
+                EXPECT(ok);
+            }
+            bool pad_zero = true;
+            for (size_t slot = n; slot < n_pad; ++slot) pad_zero = pad_zero && ids[vk::order::interleaved(slot)] == 0;
+            EXPECT(pad_zero);
+        }
+}
+
+CASE("slot order: the order lowers the LDS bank load of uniform random codes") {
+    const size_t n = 2 * 65536, m = 16;
+    const std::vector<uint8_t> codes = random_codes(n, m, 99);
+    const std::vector<uint16_t> ids = vk::order::slot_ids(codes.data(), n, m, n, 2);
+    const double natural = bank_load(codes, n, m, [](size_t slot) { return slot; });
+    const double ordered = bank_load(codes, n, m, [&](size_t slot) {
+        return slot / vk::order::kRun * vk::order::kRun + ids[vk::order::interleaved(slot)];
+    });
+    std::printf("    bank load: vector order %.3f, slot order %.3f\n", natural, ordered);
+    EXPECT(natural > 2.8 && ordered < 2.3);
+}

@@ -17,6 +17,7 @@
 
 #include "kernels.hpp"
 #include "planning.hpp"
+#include "slot_order.hpp"
 #include "veckern/veckern.h"
 
 #define VK_EXPORT extern "C" __attribute__((visibility("default")))
@@ -229,35 +230,6 @@ void fill_device_info(int device, vk_device_info* out) {
     out->warp_size = p.warpSize;
     out->l2_bytes = static_cast<size_t>(p.l2CacheSize);
     out->total_mem_bytes = p.totalGlobalMem;
-}
-
-// Slot order of the fused scans' code layout: within each run of 65536 slots, the run's vectors sorted by their
-// first two code bytes (a counting sort, on the host while the codes are at hand). Neighbouring vectors then often
-// share a code byte, and lanes of one LDS pass that read the same table entry are served by one broadcast instead
-// of queueing on one bank group: 1M vectors of 1000 Gaussian clusters, m = 16, nq = 1000: 1.28 -> 0.84 ms per
-// search; uniform random codes gain less (only the first sub-space's equal bytes line up). The result holds, per
-// slot, its vector's index within the run, interleaved by four tiles ([tile / 4][lane][tile % 4]); padding slots
-// (n .. n_pad) hold 0 and are never read as vectors.
-std::vector<uint16_t> sorted_slot_ids(const uint8_t* codes, size_t n, size_t m, size_t n_pad) {
-    constexpr size_t kRun = 65536;
-    std::vector<uint16_t> ids(n_pad, 0);
-    std::vector<uint32_t> start(kRun + 1);
-    for (size_t r0 = 0; r0 < n; r0 += kRun) {
-        const size_t len = std::min(kRun, n - r0);
-        auto key = [&](size_t i) {
-            const uint8_t* row = codes + (r0 + i) * m;
-            return (static_cast<uint32_t>(row[0]) << 8) | (m > 1 ? row[1] : 0u);
-        };
-        std::fill(start.begin(), start.end(), 0u);
-        for (size_t i = 0; i < len; ++i) ++start[key(i) + 1];
-        for (size_t b = 0; b < kRun; ++b) start[b + 1] += start[b];
-        for (size_t i = 0; i < len; ++i) {
-            const size_t slot = r0 + start[key(i)]++;
-            const size_t tile = slot / 64, lane = slot % 64;
-            ids[(tile / 4) * 256 + lane * 4 + tile % 4] = static_cast<uint16_t>(i);
-        }
-    }
-    return ids;
 }
 
 // Per-device state of the allocation-free search. `lock` serialises its calls on one device (they share the
@@ -835,8 +807,8 @@ VK_EXPORT int vk_searcher_create(const float* centroids, size_t d, size_t m, con
         VK_HIP(hipMemcpy(s->centroids.get(), centroids, m * vk::KSUB * (d / m) * sizeof(float), hipMemcpyHostToDevice));
         s->codes.ensure(n * m);
         VK_HIP(hipMemcpy(s->codes.get(), codes, n * m, hipMemcpyHostToDevice));
-        if (m % 16 == 0) {
-            const std::vector<uint16_t> order = sorted_slot_ids(codes, n, m, static_cast<size_t>(s->n_pad));
+        if (m % 16 == 0) {  // the slot order of the fused scans' layout (slot_order.hpp)
+            const std::vector<uint16_t> order = vk::order::slot_ids(codes, n, m, static_cast<size_t>(s->n_pad));
             s->slot_ids.ensure(order.size());
             VK_HIP(hipMemcpy(s->slot_ids.get(), order.data(), order.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
         }

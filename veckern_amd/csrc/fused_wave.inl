@@ -14,7 +14,10 @@
 // b64 / b128 at ((s * 256 + c) * QG * entry bytes) returns the entries of all QG queries for code byte c.
 // Measured on MI355X with uniform random bytes, a wave64 ds_read_b128 costs about 12 CU cycles against 6.4 for
 // b32, so 16-byte entry groups give ~2.1x the lookups per cycle of one fp32 table per query. NG groups share
-// every code load. fp16 tables put 8 queries in one 16-byte read.
+// every code load. fp16 tables put 8 queries in one 16-byte read. Most of those 12 cycles are bank conflicts within
+// the read's four 16-lane passes; the exhaustive scans read codes in a slot order (slot_order.hpp) that puts
+// vectors sharing code bytes in the same passes (one broadcast per shared entry) and spreads the rest over the bank
+// groups, and the vector ids travel beside the codes (SlotIds).
 //
 // Exactness. Each query's distance is summed in fp32 in sub-space order s = 0..m-1 from 0.f, exactly like the
 // CPU reference (cpu_ref.cpp:46-49), so fp32-table distances are bit-identical to the CPU's and ids agree exactly
