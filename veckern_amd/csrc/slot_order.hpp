@@ -40,37 +40,36 @@ inline size_t interleaved(size_t slot) {
 }
 
 // Deals one full block's vectors (run-relative indices, in sorted order) to its 16 passes; `out` receives them in
-// slot order (pass p holds slots 16p .. 16p+15). `present` and `groups` are scratch of 16*m*4 and 16*m*16 entries.
+// slot order (pass p holds slots 16p .. 16p+15). Scratch: `present[s * 256 + e]`, the passes (bit p) that already
+// read entry e of sub-space s, and `groups[(s * 16 + g) * 16 + p]`, pass p's distinct entries in bank group g of
+// sub-space s; the costs of all 16 passes are summed side by side (the compiler vectorises the pass loop).
 inline void deal_block(const uint8_t* run_codes, size_t m, const uint32_t* vec, uint32_t* out,
-                       std::vector<uint64_t>& present, std::vector<uint8_t>& groups) {
-    present.assign(static_cast<size_t>(kPasses) * m * 4, 0);
-    groups.assign(static_cast<size_t>(kPasses) * m * 16, 0);
+                       std::vector<uint16_t>& present, std::vector<uint8_t>& groups) {
+    present.assign(m * 256, 0);
+    groups.assign(m * 16 * kPasses, 0);
     int fill[kPasses] = {};
     for (size_t i = 0; i < kBlock; ++i) {
         const uint8_t* row = run_codes + static_cast<size_t>(vec[i]) * m;
-        int best = -1;
-        unsigned best_cost = UINT_MAX;
-        for (int p = 0; p < kPasses && best_cost > 0; ++p) {
-            if (fill[p] == kLanes) continue;
-            unsigned cost = 0;
-            for (size_t s = 0; s < m; ++s) {
-                const unsigned e = row[s];
-                const size_t ps = static_cast<size_t>(p) * m + s;
-                if ((present[ps * 4 + (e >> 6)] >> (e & 63)) & 1) continue;
-                cost += groups[ps * 16 + (e & 15)];
-            }
-            if (cost < best_cost) {
-                best_cost = cost;
-                best = p;
-            }
-        }
+        uint16_t cost[kPasses] = {};
         for (size_t s = 0; s < m; ++s) {
             const unsigned e = row[s];
-            const size_t ps = static_cast<size_t>(best) * m + s;
-            uint64_t& word = present[ps * 4 + (e >> 6)];
-            if ((word >> (e & 63)) & 1) continue;
-            word |= uint64_t{1} << (e & 63);
-            ++groups[ps * 16 + (e & 15)];
+            const unsigned mask = present[s * 256 + e];
+            const uint8_t* g = &groups[(s * 16 + (e & 15)) * kPasses];
+            for (int p = 0; p < kPasses; ++p) cost[p] += ((mask >> p) & 1u) ? 0 : g[p];
+        }
+        int best = -1;
+        unsigned best_cost = UINT_MAX;
+        for (int p = 0; p < kPasses; ++p)
+            if (fill[p] < kLanes && cost[p] < best_cost) {
+                best_cost = cost[p];
+                best = p;
+            }
+        for (size_t s = 0; s < m; ++s) {
+            const unsigned e = row[s];
+            uint16_t& mask = present[s * 256 + e];
+            if ((mask >> best) & 1u) continue;
+            mask = static_cast<uint16_t>(mask | (1u << best));
+            ++groups[(s * 16 + (e & 15)) * kPasses + best];
         }
         out[best * kLanes + fill[best]++] = vec[i];
     }
@@ -110,7 +109,7 @@ constexpr unsigned kDealMinDistinct = 8;
 // The slot ids of runs [run_lo, run_hi) into `ids` (sized n_pad). Codes row-major n x m.
 inline void order_runs(const uint8_t* codes, size_t n, size_t m, size_t run_lo, size_t run_hi, uint16_t* ids) {
     std::vector<uint32_t> start(kRun + 1), sorted(kRun), dealt(kBlock);
-    std::vector<uint64_t> present;
+    std::vector<uint16_t> present;
     std::vector<uint8_t> groups;
     for (size_t r = run_lo; r < run_hi; ++r) {
         const size_t r0 = r * kRun, len = std::min(kRun, n - r0);
