@@ -139,6 +139,36 @@ def test_single_query_final_merge_paths(family):
             assert_same(got_d, got_i, orc.adc_search(centroids, d, codes, queries[:1], k), f"{family} k={k} bpq={bpq}")
 
 
+@pytest.mark.parametrize("variant", [vk.ScanVariant.FusedWarp, vk.ScanVariant.FusedWarpF16])
+def test_final_merge_bound_equal_to_the_kth_best(variant):
+    # The k best vectors each head a different block's list, so the bound (the k-th smallest head) is the k-th best
+    # itself and exactly k pairs survive the filter: the pair equal to the bound must be kept. The 16 planted
+    # vectors have first code bytes 16 apart (one per block of the sorted layout, whose blocks cover a few first-byte
+    # values each) and distances 0.05^2 .. 0.8^2, far below the random vectors' (~60).
+    rng = np.random.default_rng(17)
+    n, d, m = 300_007, 32, 16
+    centroids = rng.standard_normal((m, 256, d // m)).astype(np.float32)
+    query = rng.standard_normal((1, d)).astype(np.float32)
+    codes = rng.integers(0, 255, size=(n, m), dtype=np.uint8)  # 255 is kept for the planted vectors
+    planted = rng.choice(n, 16, replace=False)
+    sub = query[0].reshape(m, d // m)
+    centroids[1:, 255] = sub[1:]
+    for j, v in enumerate(planted):
+        centroids[0, 16 * j] = sub[0] + np.array([0.05 * (j + 1), 0.0], dtype=np.float32)
+        codes[v, 0] = 16 * j
+        codes[v, 1:] = 255
+    oracle_search = orc.adc_search_f16 if variant == vk.ScanVariant.FusedWarpF16 else orc.adc_search
+    with vk.PQSearcher(centroids, codes, d) as s:
+        for bpq in (0, 100):
+            s.set_tuning(vk.Tuning(queries_per_block=1, blocks_per_query=bpq))
+            for k in (10, 16):
+                exp = oracle_search(centroids, d, codes, query, k)
+                assert set(exp["id"][0]) == set(planted[:k])
+                got_d, got_i, _ = s.search(query, k, variant)
+                assert s.last_launch().blocks_x > 16
+                assert_same(got_d, got_i, exp, f"bpq={bpq} k={k}")
+
+
 def test_bulk_and_one_by_one_admission_agree():
     # Blocks that scan few vectors of a slab use the instance admitting candidates in bulk; above 2^18 vectors per
     # block and slab the one admitting them one by one (the headline's). 300k vectors with one block per slab take

@@ -414,7 +414,11 @@ __device__ bool merge_query_filtered(const Pair* first, int lists, int K, int k,
     }
     load_batch(0);
     wave_sort<2, false>(head);
-    if (lane == 0) bounds[wave] = lane_read_key(head, K - 1);
+    // Read with the whole wave active: inside a lane-0 branch the compiler may sink the sort's last
+    // compare-exchange into the branch, which then updates lane 0 only, and lane K-1 would still hold its value from
+    // before that step.
+    const uint64_t kth = lane_read_key(head, K - 1);
+    if (lane == 0) bounds[wave] = kth;
     if (wave == 0 && lane == 0) *count = 0u;
     __syncthreads();
     uint64_t t = bounds[0];
