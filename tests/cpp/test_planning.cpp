@@ -3,6 +3,7 @@
 // the fused scans' code layout (veckern_amd/csrc/slot_order.hpp). The blocks_x model
 // is checked against launch shapes the reference recorded on an A100 (108 SMs, 4 resident blocks per SM).
 #include <algorithm>
+#include <climits>
 #include <cstdint>
 #include <cstdio>
 #include <random>
@@ -179,41 +180,72 @@ double bank_load(const std::vector<uint8_t>& codes, size_t n, size_t m, F vec_of
 
 }  // namespace
 
-CASE("slot order: each run's slots hold every one of its vectors once; padding holds 0; threads agree") {
-    const std::pair<size_t, size_t> shapes[] = {{1, 16},      {63, 16},    {300, 16},          {4096, 32},
-                                                {65536, 16},  {65536 + 700, 16}, {3 * 65536 + 17, 16}};
+CASE("slot order: slots [0, n) hold every vector once, blocks sorted by code bytes, tiles spread; padding holds 0") {
+    const std::pair<size_t, size_t> shapes[] = {{1, 16},     {63, 16},         {300, 16},          {4096, 32},
+                                                {65536, 16}, {65536 + 700, 16}, {3 * 65536 + 17, 16}};
     for (const auto& [n, m] : shapes)
         for (int clustered : {0, 5}) {
             const std::vector<uint8_t> codes = random_codes(n, m, n * 7 + m + clustered, clustered);
             const size_t n_pad = (n + 255) / 256 * 256;
-            const std::vector<uint16_t> ids = vk::order::slot_ids(codes.data(), n, m, n_pad, 1);
+            const std::vector<uint32_t> ids = vk::order::slot_ids(codes.data(), n, m, n_pad, 1);
             EXPECT(ids == vk::order::slot_ids(codes.data(), n, m, n_pad, 3));
             EXPECT(ids.size() == n_pad);
-            for (size_t r0 = 0; r0 < n; r0 += vk::order::kRun) {
-                const size_t len = std::min(vk::order::kRun, n - r0);
-                std::vector<char> seen(len, 0);
-                bool ok = true;
-                for (size_t slot = r0; slot < r0 + len; ++slot) {
-                    const size_t v = ids[vk::order::interleaved(slot)];
-                    ok = ok && v < len && !seen[v];
-                    if (v < len) seen[v] = 1;
-                }
-                EXPECT(ok);
+            std::vector<char> seen(n, 0);
+            bool once = true;
+            for (size_t slot = 0; slot < n; ++slot) {
+                const size_t v = ids[vk::order::interleaved(slot)];
+                once = once && v < n && !seen[v];
+                if (v < n) seen[v] = 1;
             }
+            EXPECT(once);
+            // Sorted slot t sits at slot spread_slot(t): tiles of the full blocks spread, the partial block in place.
+            // Taken in sorted order block by block, every vector of a later block sorts at or after every vector of
+            // an earlier one (dealing only permutes within a block).
+            auto key = [&](size_t v) { return (uint32_t(codes[v * m]) << 24) | (uint32_t(codes[v * m + 1]) << 16) |
+                                              (uint32_t(codes[v * m + 2]) << 8) | codes[v * m + 3]; };
+            const size_t tiles = n / 256 * 4, stride = vk::order::spread_stride(tiles);
+            std::vector<char> used(n, 0);
+            bool bijective = true, sorted = true;
+            uint32_t prev_max = 0;
+            for (size_t b0 = 0; b0 < n; b0 += 256) {
+                uint32_t lo = UINT32_MAX, hi = 0;
+                for (size_t t = b0; t < std::min(n, b0 + 256); ++t) {
+                    const size_t at = vk::order::spread_slot(t, tiles, stride);
+                    bijective = bijective && at < n && !used[at];
+                    if (at >= n) continue;
+                    used[at] = 1;
+                    const uint32_t k = key(ids[vk::order::interleaved(at)]);
+                    lo = std::min(lo, k);
+                    hi = std::max(hi, k);
+                }
+                sorted = sorted && (b0 == 0 || prev_max <= lo);
+                prev_max = hi;
+            }
+            EXPECT(bijective);
+            EXPECT(sorted);
             bool pad_zero = true;
             for (size_t slot = n; slot < n_pad; ++slot) pad_zero = pad_zero && ids[vk::order::interleaved(slot)] == 0;
             EXPECT(pad_zero);
         }
 }
 
+CASE("slot order: the spread stride is coprime with the tile count and near its golden section") {
+    for (size_t full : {size_t{3}, size_t{4}, size_t{10}, size_t{256}, size_t{3906}, size_t{390625}}) {
+        const size_t s = vk::order::spread_stride(full);
+        size_t a = s, b = full;
+        while (b) { const size_t t = a % b; a = b; b = t; }
+        EXPECT(a == 1);
+        EXPECT(s >= full * 0.6 && s <= full * 0.65 + 2);
+    }
+    EXPECT(vk::order::spread_stride(1) == 1 && vk::order::spread_stride(2) == 1);
+}
+
 CASE("slot order: the order lowers the LDS bank load of uniform random codes") {
     const size_t n = 2 * 65536, m = 16;
     const std::vector<uint8_t> codes = random_codes(n, m, 99);
-    const std::vector<uint16_t> ids = vk::order::slot_ids(codes.data(), n, m, n, 2);
+    const std::vector<uint32_t> ids = vk::order::slot_ids(codes.data(), n, m, n, 2);
     const double natural = bank_load(codes, n, m, [](size_t slot) { return slot; });
-    const double ordered = bank_load(codes, n, m, [&](size_t slot) {
-        return slot / vk::order::kRun * vk::order::kRun + ids[vk::order::interleaved(slot)];
-    });
+    const double ordered = bank_load(codes, n, m, [&](size_t slot) { return size_t{ids[vk::order::interleaved(slot)]}; });
     std::printf("    bank load: vector order %.3f, slot order %.3f\n", natural, ordered);
     EXPECT(natural > 2.8 && ordered < 2.3);
 }

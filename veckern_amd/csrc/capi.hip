@@ -256,7 +256,7 @@ struct vk_searcher {
     DeviceBuffer<float> centroids, queries, lut, dists;
     DeviceBuffer<uint8_t> codes, codes_il;
     DeviceBuffer<uint4> codes_v, codes_s;  // words in vector order (v6, v7) and in sorted slot order (v8, v9)
-    DeviceBuffer<uint16_t> slot_ids;        // the sorted slot order (m % 16 == 0 only)
+    DeviceBuffer<uint32_t> slot_ids;        // the sorted slot order: the vector id of each slot (m % 16 == 0 only)
     DeviceBuffer<Pair> part, out;
     PinnedBuffer<float> staged_q;     // host-buffer searches: queries and results staged in page-locked memory
     PinnedBuffer<Pair> staged_out;
@@ -808,9 +808,9 @@ VK_EXPORT int vk_searcher_create(const float* centroids, size_t d, size_t m, con
         s->codes.ensure(n * m);
         VK_HIP(hipMemcpy(s->codes.get(), codes, n * m, hipMemcpyHostToDevice));
         if (m % 16 == 0) {  // the slot order of the fused scans' layout (slot_order.hpp)
-            const std::vector<uint16_t> order = vk::order::slot_ids(codes, n, m, static_cast<size_t>(s->n_pad));
+            const std::vector<uint32_t> order = vk::order::slot_ids(codes, n, m, static_cast<size_t>(s->n_pad));
             s->slot_ids.ensure(order.size());
-            VK_HIP(hipMemcpy(s->slot_ids.get(), order.data(), order.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
+            VK_HIP(hipMemcpy(s->slot_ids.get(), order.data(), order.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
         }
         *out = s.release();
     });

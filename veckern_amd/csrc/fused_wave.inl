@@ -484,25 +484,29 @@ __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K,
     __syncthreads();
 }
 
-// Vector ids of a granule's U tiles in the sorted code layout (exhaustive scans): per slot, the index of its vector
-// within the slot's run of 65536 slots, 16 bits, interleaved by four tiles ([tile / 4][lane][tile % 4]), so one
-// load of 2U bytes gives a lane the ids of its U tiles (a granule's tiles start at a multiple of U, and U <= 4).
+// Vector ids of a granule's U tiles in the sorted code layout (exhaustive scans): per slot, its vector's id,
+// interleaved by four tiles ([tile / 4][lane][tile % 4]), so one load of 4U bytes gives a lane the ids of its U
+// tiles (a granule's tiles start at a multiple of U, and U <= 4).
 template <int U>
 struct SlotIds {
-    uint32_t w[U == 4 ? 2 : 1];
-    __device__ __forceinline__ void load(const uint16_t* slot_ids, int64_t tile0, int lane) {
-        const uint16_t* p = slot_ids + (tile0 >> 2) * 256 + lane * 4 + (tile0 & 3);
+    uint32_t w[U];
+    __device__ __forceinline__ void load(const uint32_t* slot_ids, int64_t tile0, int lane) {
+        const uint32_t* p = slot_ids + (tile0 >> 2) * 256 + lane * 4 + (tile0 & 3);
         if constexpr (U == 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p);
+            w[0] = v.x;
+            w[1] = v.y;
+            w[2] = v.z;
+            w[3] = v.w;
+        } else if constexpr (U == 2) {
             const uint2 v = *reinterpret_cast<const uint2*>(p);
             w[0] = v.x;
             w[1] = v.y;
-        } else if constexpr (U == 2) {
-            w[0] = *reinterpret_cast<const uint32_t*>(p);
         } else {
             w[0] = *p;
         }
     }
-    __device__ __forceinline__ uint32_t get(int u) const { return (w[u >> 1] >> (16 * (u & 1))) & 0xffffu; }
+    __device__ __forceinline__ uint32_t get(int u) const { return w[u]; }
 };
 
 // QG: queries per table (1, 2, 4; 8 with fp16 entries). NG: tables per block (1, 2). U: 64-vector tiles per wave
@@ -834,10 +838,9 @@ __global__ void __launch_bounds__(T)
                     id = static_cast<uint32_t>(vid);
                     valid = __builtin_amdgcn_ballot_w64(vid >= 0);
                 } else {
-                    // Slots [0, n) hold real vectors in every run of the sorted layout; the id is the run's first
-                    // slot plus the vector's index within the run.
+                    // Slots [0, n) hold the real vectors of the sorted layout, each with its id beside it.
                     const uint32_t first = static_cast<uint32_t>((tile0 + u) * WAVE);
-                    id = ((first >> 16) << 16) + ids.get(u);
+                    id = ids.get(u);
                     valid = first + WAVE <= n32 ? ~uint64_t{0}
                                                 : __builtin_amdgcn_ballot_w64(first + static_cast<uint32_t>(lane) < n32);
                 }

@@ -18,9 +18,9 @@ hipError_t launch_lut(const float* queries, const float* centroids, int d, int m
 // ---- code layouts (layout.hip). n_pad is a multiple of 64; vectors past n are zero codes.
 // Word-interleaved: out[(tile * (m/16) + w) * 64 + lane] = 16 sub-codes 16w..16w+15 of vector tile*64+lane.
 hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint4* out, hipStream_t stream);
-// The word-interleaved layout in the fused scans' slot order: slot j holds vector (j / 65536) * 65536 +
-// slot_ids[j's interleaved position]; slots [n, n_pad) are zero.
-hipError_t launch_build_sorted_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, const uint16_t* slot_ids,
+// The word-interleaved layout in the fused scans' slot order: slot j holds vector slot_ids[j's interleaved
+// position]; slots [n, n_pad) are zero.
+hipError_t launch_build_sorted_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, const uint32_t* slot_ids,
                                      uint4* out, hipStream_t stream);
 // Byte-interleaved: out[(tile * m + s) * 64 + lane] = sub-code s of vector tile*64+lane.
 hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint8_t* out,
@@ -34,8 +34,8 @@ struct WaveScanArgs {
     const float* centroids;  // [m][256][d / m]
     const uint4* codes;      // word-interleaved, padded to a multiple of 256 vectors (exhaustive scans: the sorted
                              // layout, slot order given by slot_ids)
-    const uint16_t* slot_ids;  // exhaustive scans: per slot, its vector's index within the slot's run of 65536
-                               // slots, interleaved by four tiles ([tile / 4][lane][tile % 4])
+    const uint32_t* slot_ids;  // exhaustive scans: per slot, its vector's id, interleaved by four tiles
+                               // ([tile / 4][lane][tile % 4])
     int64_t n;
     int d;
     int m;

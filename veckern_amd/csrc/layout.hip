@@ -42,21 +42,21 @@ hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_
 
 __global__ void __launch_bounds__(256)
     build_sorted_words_kernel(const uint8_t* __restrict__ codes, int64_t n, int words, int64_t total,
-                              const uint16_t* __restrict__ slot_ids, uint4* __restrict__ out) {
+                              const uint32_t* __restrict__ slot_ids, uint4* __restrict__ out) {
     for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total;
          o += static_cast<int64_t>(gridDim.x) * 256) {
         const int64_t lane = o % WAVE, w = (o / WAVE) % words, tile = o / (static_cast<int64_t>(WAVE) * words);
         const int64_t slot = tile * WAVE + lane;
         uint4 v = make_uint4(0, 0, 0, 0);
         if (slot < n) {
-            const int64_t i = ((slot >> 16) << 16) + slot_ids[(tile >> 2) * 256 + lane * 4 + (tile & 3)];
+            const int64_t i = slot_ids[(tile >> 2) * 256 + lane * 4 + (tile & 3)];
             v = *reinterpret_cast<const uint4*>(codes + (i * words + w) * 16);
         }
         out[o] = v;
     }
 }
 
-hipError_t launch_build_sorted_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, const uint16_t* slot_ids,
+hipError_t launch_build_sorted_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, const uint32_t* slot_ids,
                                      uint4* out, hipStream_t stream) {
     const int words = m / 16;
     const int64_t total = n_pad * words;

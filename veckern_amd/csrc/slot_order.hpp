@@ -6,18 +6,29 @@
 // 4 cycles per CU when every pass has 16 distinct bank groups and about the sum over its passes of the largest
 // number of distinct entries in one group otherwise (uniform random entries: ~3 per pass, ~12 cycles).
 //
-// The order has two levels. Within each run of 65536 slots, the run's vectors are sorted by their first two code
-// bytes (a counting sort): vectors that share code bytes then sit in the same passes, where their shared entries
-// are broadcasts. Within each full block of 256 slots (16 passes, four tiles), the block's vectors are then dealt
+// The order has three levels. All vectors are sorted by their first four code bytes (a radix sort): vectors that
+// share code bytes then sit in the same passes, where their shared entries are broadcasts.
+// Within each full block of 256 slots (16 passes, four tiles), the block's vectors are then dealt
 // to passes first-fit: in sorted order, each goes to the pass (with room) where its entries add the fewest distinct
 // entries to bank groups already in use; entries already present cost nothing. Only blocks with little sharing are
 // dealt (kDealMinDistinct), and only where it lowers the block's bank load. Mean of the largest distinct-entry count
 // per (pass, sub-space): uniform random codes 2.92 in vector order, 2.70 sorted, 2.14 sorted and dealt (100M uniform
 // codes, nq=1000: 116.4 -> 106.0 ms per search).
+// Last, the tiles of the full blocks are spread over the layout: sorted tile t (64 slots, four passes) goes to tile
+// position t * s mod T (T tiles in full blocks, s the integer nearest T / golden ratio that is coprime with T); the
+// partial last block stays last. A scan block's range of slots then holds tiles from all over the sorted order, and
+// a granule's U consecutive tiles come from far-apart parts of it, as in vector order. Kept in sorted order, a scan
+// block covers a narrow range of leading code bytes and a granule a run of near-identical vectors: the wave lists
+// admit candidates in bursts, and the blocks nearest the query take many more inserts than the rest. Measured scan
+// time (ms) of blocks in sorted order / spread by 256-slot block / by 16-slot pass / by 64-slot tile: 1M x nq=1000
+// 0.750 / 0.730 / 0.735 / 0.711, fp16 tables 0.896 / 0.837 / 0.762 / 0.799; 10M x nq=1000 5.91 / 5.91 / 6.28 / 5.88;
+// 10M x one query 0.059 / 0.056 / 0.048 / 0.047; 100M x nq=1000 100.3 / 99.9 / 99.7 / 99.8.
 //
-// The result holds, per slot, its vector's index within its run (16 bits), interleaved by four tiles:
-// ids[(tile / 4) * 256 + lane * 4 + tile % 4] for slot = tile * 64 + lane. Slots [0, n) hold every vector exactly
-// once, each run's own; padding slots [n, n_pad) hold 0 and are never read as vectors.
+// The result holds, per slot, its vector's id, interleaved by four tiles: ids[(tile / 4) * 256 + lane * 4 + tile % 4]
+// for slot = tile * 64 + lane. Slots [0, n) hold every vector exactly once; padding slots [n, n_pad) hold 0 and are
+// never read as vectors. Sorting only within runs of 65536 slots (16-bit ids), with no spread, measured 1M x
+// nq=1000 0.767 ms, fp16 tables 0.787, 10M 6.83, 10M x one query 0.048, 100M 105.7: whole clusters line up only in a
+// global order.
 #pragma once
 
 #include <algorithm>
@@ -25,11 +36,11 @@
 #include <cstddef>
 #include <cstdint>
 #include <thread>
+#include <utility>
 #include <vector>
 
 namespace vk::order {
 
-constexpr size_t kRun = 65536;   // slots per run: a vector's index within its run fits in 16 bits
 constexpr size_t kBlock = 256;   // slots dealt together: 16 passes of 16 lanes, four tiles
 constexpr int kPasses = 16;
 constexpr int kLanes = 16;
@@ -39,17 +50,17 @@ inline size_t interleaved(size_t slot) {
     return (tile / 4) * 256 + lane * 4 + tile % 4;
 }
 
-// Deals one full block's vectors (run-relative indices, in sorted order) to its 16 passes; `out` receives them in
+// Deals one full block's vectors (ids, in sorted order) to its 16 passes; `out` receives them in
 // slot order (pass p holds slots 16p .. 16p+15). Scratch: `present[s * 256 + e]`, the passes (bit p) that already
 // read entry e of sub-space s, and `groups[(s * 16 + g) * 16 + p]`, pass p's distinct entries in bank group g of
 // sub-space s; the costs of all 16 passes are summed side by side (the compiler vectorises the pass loop).
-inline void deal_block(const uint8_t* run_codes, size_t m, const uint32_t* vec, uint32_t* out,
+inline void deal_block(const uint8_t* codes, size_t m, const uint32_t* vec, uint32_t* out,
                        std::vector<uint16_t>& present, std::vector<uint8_t>& groups) {
     present.assign(m * 256, 0);
     groups.assign(m * 16 * kPasses, 0);
     int fill[kPasses] = {};
     for (size_t i = 0; i < kBlock; ++i) {
-        const uint8_t* row = run_codes + static_cast<size_t>(vec[i]) * m;
+        const uint8_t* row = codes + static_cast<size_t>(vec[i]) * m;
         uint16_t cost[kPasses] = {};
         for (size_t s = 0; s < m; ++s) {
             const unsigned e = row[s];
@@ -81,7 +92,7 @@ inline void deal_block(const uint8_t* run_codes, size_t m, const uint32_t* vec, 
 struct BlockStats {
     unsigned load = 0, distinct = 0;
 };
-inline BlockStats block_stats(const uint8_t* run_codes, size_t m, const uint32_t* block) {
+inline BlockStats block_stats(const uint8_t* codes, size_t m, const uint32_t* block) {
     BlockStats st;
     for (int p = 0; p < kPasses; ++p)
         for (size_t s = 0; s < m; ++s) {
@@ -89,7 +100,7 @@ inline BlockStats block_stats(const uint8_t* run_codes, size_t m, const uint32_t
             uint8_t groups[16] = {};
             unsigned mx = 0;
             for (int l = 0; l < kLanes; ++l) {
-                const unsigned e = run_codes[static_cast<size_t>(block[p * kLanes + l]) * m + s];
+                const unsigned e = codes[static_cast<size_t>(block[p * kLanes + l]) * m + s];
                 if ((seen[e >> 6] >> (e & 63)) & 1) continue;
                 seen[e >> 6] |= uint64_t{1} << (e & 63);
                 mx = std::max<unsigned>(mx, ++groups[e & 15]);
@@ -106,51 +117,127 @@ inline BlockStats block_stats(const uint8_t* run_codes, size_t m, const uint32_t
 // are split up).
 constexpr unsigned kDealMinDistinct = 8;
 
-// The slot ids of runs [run_lo, run_hi) into `ids` (sized n_pad). Codes row-major n x m.
-inline void order_runs(const uint8_t* codes, size_t n, size_t m, size_t run_lo, size_t run_hi, uint16_t* ids) {
-    std::vector<uint32_t> start(kRun + 1), sorted(kRun), dealt(kBlock);
+// Runs f(t) for t in [0, threads) on host threads (inline when threads <= 1).
+template <typename F>
+inline void parallel(unsigned threads, F&& f) {
+    if (threads <= 1) {
+        f(0u);
+        return;
+    }
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < threads; ++t) pool.emplace_back(f, t);
+    for (std::thread& th : pool) th.join();
+}
+
+// All vector ids sorted by their first four code bytes (missing bytes count as 0): (key << 32 | id) pairs, then an
+// LSD radix sort on the key's four bytes (stable, so equal keys keep id order), each pass split over `threads`
+// contiguous chunks (per-chunk digit counts give every chunk its own output offsets).
+inline std::vector<uint32_t> sorted_ids(const uint8_t* codes, size_t n, size_t m, unsigned threads) {
+    std::vector<uint64_t> a(n), t(n);
+    auto chunk = [&](unsigned c) { return std::pair<size_t, size_t>{n * c / threads, n * (c + 1) / threads}; };
+    parallel(threads, [&](unsigned c) {
+        const auto [lo, hi] = chunk(c);
+        for (size_t i = lo; i < hi; ++i) {
+            const uint8_t* row = codes + i * m;
+            uint32_t key = 0;
+            for (size_t b = 0; b < 4; ++b) key = (key << 8) | (b < m ? row[b] : 0u);
+            a[i] = (static_cast<uint64_t>(key) << 32) | static_cast<uint32_t>(i);
+        }
+    });
+    std::vector<size_t> count(static_cast<size_t>(threads) * 256);
+    for (int shift = 32; shift < 64; shift += 8) {
+        std::fill(count.begin(), count.end(), size_t{0});
+        parallel(threads, [&](unsigned c) {
+            const auto [lo, hi] = chunk(c);
+            size_t* cnt = count.data() + static_cast<size_t>(c) * 256;
+            for (size_t i = lo; i < hi; ++i) ++cnt[(a[i] >> shift) & 0xffu];
+        });
+        size_t at = 0;  // digit-major, then chunk: chunk c's entries of digit d follow those of chunks < c
+        for (int d = 0; d < 256; ++d)
+            for (unsigned c = 0; c < threads; ++c) {
+                size_t& slot = count[static_cast<size_t>(c) * 256 + d];
+                const size_t k = slot;
+                slot = at;
+                at += k;
+            }
+        parallel(threads, [&](unsigned c) {
+            const auto [lo, hi] = chunk(c);
+            size_t* next = count.data() + static_cast<size_t>(c) * 256;
+            for (size_t i = lo; i < hi; ++i) t[next[(a[i] >> shift) & 0xffu]++] = a[i];
+        });
+        a.swap(t);
+    }
+    std::vector<uint32_t> ids(n);
+    for (size_t i = 0; i < n; ++i) ids[i] = static_cast<uint32_t>(a[i]);
+    return ids;
+}
+
+// Multiplier of the spread over `count` tiles: the integer nearest count / golden ratio, raised until coprime with
+// `count` (so that t -> t * stride mod count is a bijection); 1 for fewer than three tiles.
+inline size_t spread_stride(size_t count) {
+    if (count < 3) return 1;
+    auto gcd = [](size_t a, size_t b) {
+        while (b) {
+            const size_t t = a % b;
+            a = b;
+            b = t;
+        }
+        return a;
+    };
+    size_t s = static_cast<size_t>(static_cast<double>(count) * 0.6180339887498949 + 0.5);
+    while (gcd(s, count) != 1) ++s;
+    return s;
+}
+
+constexpr size_t kTile = 64;  // slots of one wave step
+
+// Slot of sorted slot t: in the full blocks' `tiles` tiles, its tile spread by `stride`; past them, t itself.
+inline size_t spread_slot(size_t t, size_t tiles, size_t stride) {
+    return t < tiles * kTile ? (t / kTile) * stride % tiles * kTile + t % kTile : t;
+}
+
+// Blocks [blk_lo, blk_hi) of the sorted ids: dealt where that pays, then written to `ids` at their spread slots. A
+// full block's code rows are first gathered into a local copy, which the statistics and the dealing then read.
+inline void order_blocks(const uint8_t* codes, size_t n, size_t m, const uint32_t* sorted, size_t blk_lo,
+                         size_t blk_hi, uint32_t* ids) {
+    const size_t tiles = n / kBlock * (kBlock / kTile), stride = spread_stride(tiles);
+    auto place = [&](size_t t) { return interleaved(spread_slot(t, tiles, stride)); };
+    std::vector<uint32_t> local(kBlock), dealt(kBlock);
+    std::vector<uint8_t> rows(kBlock * m);
     std::vector<uint16_t> present;
     std::vector<uint8_t> groups;
-    for (size_t r = run_lo; r < run_hi; ++r) {
-        const size_t r0 = r * kRun, len = std::min(kRun, n - r0);
-        const uint8_t* run_codes = codes + r0 * m;
-        auto key = [&](size_t i) {
-            const uint8_t* row = run_codes + i * m;
-            return (static_cast<uint32_t>(row[0]) << 8) | (m > 1 ? row[1] : 0u);
-        };
-        std::fill(start.begin(), start.end(), 0u);
-        for (size_t i = 0; i < len; ++i) ++start[key(i) + 1];
-        for (size_t b = 0; b < kRun; ++b) start[b + 1] += start[b];
-        for (size_t i = 0; i < len; ++i) sorted[start[key(i)]++] = static_cast<uint32_t>(i);
-        for (size_t b0 = 0; b0 < len; b0 += kBlock) {
-            const uint32_t* block = sorted.data() + b0;
-            if (b0 + kBlock <= len) {
-                const BlockStats st = block_stats(run_codes, m, block);
-                if (st.distinct >= kDealMinDistinct * kPasses * m) {
-                    deal_block(run_codes, m, block, dealt.data(), present, groups);
-                    if (block_stats(run_codes, m, dealt.data()).load < st.load) block = dealt.data();
+    for (size_t i = 0; i < kBlock; ++i) local[i] = static_cast<uint32_t>(i);
+    for (size_t blk = blk_lo; blk < blk_hi; ++blk) {
+        const size_t b0 = blk * kBlock;
+        const size_t cnt = std::min(kBlock, n - b0);
+        const uint32_t* block = sorted + b0;
+        if (cnt == kBlock) {
+            for (size_t i = 0; i < kBlock; ++i)
+                std::copy(codes + static_cast<size_t>(block[i]) * m, codes + (static_cast<size_t>(block[i]) + 1) * m,
+                          rows.begin() + i * m);
+            const BlockStats st = block_stats(rows.data(), m, local.data());
+            if (st.distinct >= kDealMinDistinct * kPasses * m) {
+                deal_block(rows.data(), m, local.data(), dealt.data(), present, groups);
+                if (block_stats(rows.data(), m, dealt.data()).load < st.load) {
+                    for (size_t j = 0; j < kBlock; ++j) ids[place(b0 + j)] = block[dealt[j]];
+                    continue;
                 }
             }
-            const size_t cnt = std::min(kBlock, len - b0);
-            for (size_t j = 0; j < cnt; ++j) ids[interleaved(r0 + b0 + j)] = static_cast<uint16_t>(block[j]);
         }
+        for (size_t j = 0; j < cnt; ++j) ids[place(b0 + j)] = block[j];
     }
 }
 
-// Slot ids of the whole layout; runs are ordered on up to `threads` host threads.
-inline std::vector<uint16_t> slot_ids(const uint8_t* codes, size_t n, size_t m, size_t n_pad, unsigned threads = 0) {
-    std::vector<uint16_t> ids(n_pad, 0);
-    const size_t runs = (n + kRun - 1) / kRun;
+// Slot ids of the whole layout; blocks are ordered on up to `threads` host threads.
+inline std::vector<uint32_t> slot_ids(const uint8_t* codes, size_t n, size_t m, size_t n_pad, unsigned threads = 0) {
+    std::vector<uint32_t> ids(n_pad, 0);
+    const size_t blocks = (n + kBlock - 1) / kBlock;
     if (threads == 0) threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-    threads = static_cast<unsigned>(std::min<size_t>(threads, runs));
-    if (threads <= 1) {
-        order_runs(codes, n, m, 0, runs, ids.data());
-        return ids;
-    }
-    std::vector<std::thread> pool;
-    for (unsigned t = 0; t < threads; ++t)
-        pool.emplace_back(order_runs, codes, n, m, runs * t / threads, runs * (t + 1) / threads, ids.data());
-    for (std::thread& th : pool) th.join();
+    threads = static_cast<unsigned>(std::max<size_t>(1, std::min<size_t>(threads, (blocks + 63) / 64)));
+    const std::vector<uint32_t> sorted = sorted_ids(codes, n, m, threads);
+    parallel(threads, [&](unsigned t) {
+        order_blocks(codes, n, m, sorted.data(), blocks * t / threads, blocks * (t + 1) / threads, ids.data());
+    });
     return ids;
 }
 
