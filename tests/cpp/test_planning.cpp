@@ -240,6 +240,27 @@ CASE("slot order: the spread stride is coprime with the tile count and near its 
     EXPECT(vk::order::spread_stride(1) == 1 && vk::order::spread_stride(2) == 1);
 }
 
+CASE("slot order: an inverted list's members sorted by code key, equal keys in id order") {
+    const size_t n = 5000, m = 16;
+    const std::vector<uint8_t> codes = random_codes(n, m, 7, 5);
+    std::vector<int32_t> members;
+    for (int32_t i = 3; i < static_cast<int32_t>(n); i += 3) members.push_back(i);
+    std::vector<int32_t> sorted = members;
+    std::vector<uint64_t> scratch;
+    vk::order::sort_members(codes.data(), m, sorted.data(), sorted.size(), scratch);
+    std::vector<int32_t> a = members, b = sorted;
+    std::sort(a.begin(), a.end());
+    std::sort(b.begin(), b.end());
+    EXPECT(a == b);
+    bool ordered = true;
+    for (size_t j = 1; j < sorted.size(); ++j) {
+        const uint32_t k0 = vk::order::code_key(&codes[sorted[j - 1] * m], m), k1 = vk::order::code_key(&codes[sorted[j] * m], m);
+        ordered = ordered && (k0 < k1 || (k0 == k1 && sorted[j - 1] < sorted[j]));
+    }
+    EXPECT(ordered);
+    EXPECT(vk::order::code_key(&codes[0], 2) == ((uint32_t(codes[0]) << 24) | (uint32_t(codes[1]) << 16)));
+}
+
 CASE("slot order: the order lowers the LDS bank load of uniform random codes") {
     const size_t n = 2 * 65536, m = 16;
     const std::vector<uint8_t> codes = random_codes(n, m, 99);

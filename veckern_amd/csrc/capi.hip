@@ -1096,7 +1096,7 @@ VK_EXPORT int vk_ivf_create(const float* coarse, size_t nlist, const float* cent
         v->m = m;
         v->nlist = nlist;
         require(m * vk::KSUB * sizeof(float) <= v->info.max_smem_per_block, "LUT does not fit in LDS");
-        // group the vectors by list (stable in id order), each list padded to a multiple of 256 vectors
+        // group the vectors by list, each list padded to a multiple of 256 vectors
         std::vector<int64_t> sizes(nlist, 0);
         for (size_t i = 0; i < n; ++i) {
             require(list_ids[i] >= 0 && static_cast<size_t>(list_ids[i]) < nlist, "list id out of range");
@@ -1109,11 +1109,18 @@ VK_EXPORT int vk_ivf_create(const float* coarse, size_t nlist, const float* cent
         std::vector<int32_t> ids(static_cast<size_t>(std::max<int64_t>(padded, 1)), -1);
         std::vector<int64_t> fill(nlist);
         for (size_t l = 0; l < nlist; ++l) fill[l] = v->list_tile_h[l] * vk::WAVE;
-        for (size_t i = 0; i < n; ++i) {
-            const int64_t pos = fill[list_ids[i]]++;
-            std::memcpy(rows.data() + pos * m, codes + i * m, m);
-            ids[pos] = static_cast<int32_t>(i);
-        }
+        for (size_t i = 0; i < n; ++i) ids[fill[list_ids[i]]++] = static_cast<int32_t>(i);
+        // Within each list the members are ordered by their code bytes (slot_order.hpp), then their rows copied.
+        const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+        vk::order::parallel(threads, [&](unsigned t) {
+            std::vector<uint64_t> scratch;
+            for (size_t l = t; l < nlist; l += threads) {
+                const int64_t base = v->list_tile_h[l] * vk::WAVE;
+                vk::order::sort_members(codes, m, ids.data() + base, static_cast<size_t>(sizes[l]), scratch);
+                for (int64_t j = 0; j < sizes[l]; ++j)
+                    std::memcpy(rows.data() + (base + j) * m, codes + static_cast<size_t>(ids[base + j]) * m, m);
+            }
+        });
         VK_HIP(hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking));
         v->coarse.ensure(nlist * d);
         VK_HIP(hipMemcpy(v->coarse.get(), coarse, nlist * d * sizeof(float), hipMemcpyHostToDevice));

@@ -129,6 +129,13 @@ inline void parallel(unsigned threads, F&& f) {
     for (std::thread& th : pool) th.join();
 }
 
+// Sort key of a code row: its first four bytes, big-endian (missing bytes count as 0).
+inline uint32_t code_key(const uint8_t* row, size_t m) {
+    uint32_t key = 0;
+    for (size_t b = 0; b < 4; ++b) key = (key << 8) | (b < m ? row[b] : 0u);
+    return key;
+}
+
 // All vector ids sorted by their first four code bytes (missing bytes count as 0): (key << 32 | id) pairs, then an
 // LSD radix sort on the key's four bytes (stable, so equal keys keep id order), each pass split over `threads`
 // contiguous chunks (per-chunk digit counts give every chunk its own output offsets).
@@ -138,10 +145,7 @@ inline std::vector<uint32_t> sorted_ids(const uint8_t* codes, size_t n, size_t m
     parallel(threads, [&](unsigned c) {
         const auto [lo, hi] = chunk(c);
         for (size_t i = lo; i < hi; ++i) {
-            const uint8_t* row = codes + i * m;
-            uint32_t key = 0;
-            for (size_t b = 0; b < 4; ++b) key = (key << 8) | (b < m ? row[b] : 0u);
-            a[i] = (static_cast<uint64_t>(key) << 32) | static_cast<uint32_t>(i);
+            a[i] = (static_cast<uint64_t>(code_key(codes + i * m, m)) << 32) | static_cast<uint32_t>(i);
         }
     });
     std::vector<size_t> count(static_cast<size_t>(threads) * 256);
@@ -239,6 +243,19 @@ inline std::vector<uint32_t> slot_ids(const uint8_t* codes, size_t n, size_t m, 
         order_blocks(codes, n, m, sorted.data(), blocks * t / threads, blocks * (t + 1) / threads, ids.data());
     });
     return ids;
+}
+
+// Members of one inverted list (vector ids), reordered by their code keys, equal keys in id order. The IVF scan
+// reads one query's table per block (4-byte entries, one per lane): members that share code bytes then read shared
+// table entries, which the LDS serves as broadcasts. Neither dealt nor spread: the dealing models 16-byte reads.
+inline void sort_members(const uint8_t* codes, size_t m, int32_t* members, size_t count,
+                         std::vector<uint64_t>& scratch) {
+    scratch.resize(count);
+    for (size_t j = 0; j < count; ++j)
+        scratch[j] = (static_cast<uint64_t>(code_key(codes + static_cast<size_t>(members[j]) * m, m)) << 32) |
+                     static_cast<uint32_t>(members[j]);
+    std::sort(scratch.begin(), scratch.end());
+    for (size_t j = 0; j < count; ++j) members[j] = static_cast<int32_t>(static_cast<uint32_t>(scratch[j]));
 }
 
 }  // namespace vk::order
