@@ -240,24 +240,31 @@ CASE("slot order: the spread stride is coprime with the tile count and near its 
     EXPECT(vk::order::spread_stride(1) == 1 && vk::order::spread_stride(2) == 1);
 }
 
-CASE("slot order: an inverted list's members sorted by code key, equal keys in id order") {
-    const size_t n = 5000, m = 16;
+CASE("slot order: an inverted list's members sorted by code key (ties by id), full tiles spread") {
+    const size_t n = 30000, m = 16;
     const std::vector<uint8_t> codes = random_codes(n, m, 7, 5);
-    std::vector<int32_t> members;
-    for (int32_t i = 3; i < static_cast<int32_t>(n); i += 3) members.push_back(i);
-    std::vector<int32_t> sorted = members;
-    std::vector<uint64_t> scratch;
-    vk::order::sort_members(codes.data(), m, sorted.data(), sorted.size(), scratch);
-    std::vector<int32_t> a = members, b = sorted;
-    std::sort(a.begin(), a.end());
-    std::sort(b.begin(), b.end());
-    EXPECT(a == b);
-    bool ordered = true;
-    for (size_t j = 1; j < sorted.size(); ++j) {
-        const uint32_t k0 = vk::order::code_key(&codes[sorted[j - 1] * m], m), k1 = vk::order::code_key(&codes[sorted[j] * m], m);
-        ordered = ordered && (k0 < k1 || (k0 == k1 && sorted[j - 1] < sorted[j]));
+    for (size_t count : {size_t{0}, size_t{1}, size_t{63}, size_t{64}, size_t{200}, size_t{9999}}) {
+        std::vector<int32_t> members;
+        for (size_t i = 0; i < count; ++i) members.push_back(static_cast<int32_t>(i * 3));
+        std::vector<int32_t> placed = members;
+        std::vector<uint64_t> scratch;
+        vk::order::order_members(codes.data(), m, placed.data(), placed.size(), scratch);
+        std::vector<int32_t> a = members, b = placed;
+        std::sort(a.begin(), a.end());
+        std::sort(b.begin(), b.end());
+        EXPECT(a == b);
+        // undo the spread and check the sorted order
+        const size_t tiles = count / 64, stride = vk::order::spread_stride(tiles);
+        std::vector<int32_t> sorted(count);
+        for (size_t j = 0; j < count; ++j) sorted[j] = placed[vk::order::spread_slot(j, tiles, stride)];
+        bool ordered = true;
+        for (size_t j = 1; j < count; ++j) {
+            const uint32_t k0 = vk::order::code_key(&codes[sorted[j - 1] * m], m);
+            const uint32_t k1 = vk::order::code_key(&codes[sorted[j] * m], m);
+            ordered = ordered && (k0 < k1 || (k0 == k1 && sorted[j - 1] < sorted[j]));
+        }
+        EXPECT(ordered);
     }
-    EXPECT(ordered);
     EXPECT(vk::order::code_key(&codes[0], 2) == ((uint32_t(codes[0]) << 24) | (uint32_t(codes[1]) << 16)));
 }
 

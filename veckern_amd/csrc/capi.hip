@@ -1110,13 +1110,14 @@ VK_EXPORT int vk_ivf_create(const float* coarse, size_t nlist, const float* cent
         std::vector<int64_t> fill(nlist);
         for (size_t l = 0; l < nlist; ++l) fill[l] = v->list_tile_h[l] * vk::WAVE;
         for (size_t i = 0; i < n; ++i) ids[fill[list_ids[i]]++] = static_cast<int32_t>(i);
-        // Within each list the members are ordered by their code bytes (slot_order.hpp), then their rows copied.
+        // Within each list the members are ordered by their code bytes, tiles spread (slot_order.hpp), then their
+        // rows copied.
         const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
         vk::order::parallel(threads, [&](unsigned t) {
             std::vector<uint64_t> scratch;
             for (size_t l = t; l < nlist; l += threads) {
                 const int64_t base = v->list_tile_h[l] * vk::WAVE;
-                vk::order::sort_members(codes, m, ids.data() + base, static_cast<size_t>(sizes[l]), scratch);
+                vk::order::order_members(codes, m, ids.data() + base, static_cast<size_t>(sizes[l]), scratch);
                 for (int64_t j = 0; j < sizes[l]; ++j)
                     std::memcpy(rows.data() + (base + j) * m, codes + static_cast<size_t>(ids[base + j]) * m, m);
             }

@@ -245,17 +245,23 @@ inline std::vector<uint32_t> slot_ids(const uint8_t* codes, size_t n, size_t m, 
     return ids;
 }
 
-// Members of one inverted list (vector ids), reordered by their code keys, equal keys in id order. The IVF scan
-// reads one query's table per block (4-byte entries, one per lane): members that share code bytes then read shared
-// table entries, which the LDS serves as broadcasts. Neither dealt nor spread: the dealing models 16-byte reads.
-inline void sort_members(const uint8_t* codes, size_t m, int32_t* members, size_t count,
-                         std::vector<uint64_t>& scratch) {
+// Members of one inverted list (vector ids), reordered: sorted by their code keys, equal keys in id order, then the
+// list's full 64-slot tiles spread over its tile positions as in the exhaustive layout (t -> t * s mod T; members of a
+// partial last tile stay last). The IVF scan reads one query's table per block (4-byte entries, one per lane):
+// members that share code bytes then read shared table entries, which the LDS serves as broadcasts, and the spread
+// keeps a wave's successive tiles from being near-identical runs. Not dealt: the dealing models 16-byte reads.
+// 1M vectors, 1024 lists, nq=1000: nprobe 32 scan 0.233 ms in id order, 0.218 sorted, 0.214 sorted and spread;
+// nprobe 8 0.098, 0.097, 0.092.
+inline void order_members(const uint8_t* codes, size_t m, int32_t* members, size_t count,
+                          std::vector<uint64_t>& scratch) {
     scratch.resize(count);
     for (size_t j = 0; j < count; ++j)
         scratch[j] = (static_cast<uint64_t>(code_key(codes + static_cast<size_t>(members[j]) * m, m)) << 32) |
                      static_cast<uint32_t>(members[j]);
     std::sort(scratch.begin(), scratch.end());
-    for (size_t j = 0; j < count; ++j) members[j] = static_cast<int32_t>(static_cast<uint32_t>(scratch[j]));
+    const size_t tiles = count / kTile, stride = spread_stride(tiles);
+    for (size_t j = 0; j < count; ++j)
+        members[spread_slot(j, tiles, stride)] = static_cast<int32_t>(static_cast<uint32_t>(scratch[j]));
 }
 
 }  // namespace vk::order
