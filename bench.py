@@ -295,8 +295,10 @@ def main():
         f"HBM read {hbm_gbs:.0f} GB/s")
 
     s = vk.PQSearcher(centroids, codes, d)
-    if args.queries_per_block is None:  # fp16 tables: 8 queries share one 16-byte table read
-        args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config == "A" else 4)
+    # Queries per block: fp16 tables put 8 queries in one 16-byte table read; 100k and 1M at m=32 (k=100) run faster
+    # at 2 (measured: m=32 2.05 ms at Q=2 against 2.18 at Q=4, the 64 KB tables leaving room for two blocks per CU)
+    if args.queries_per_block is None:
+        args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config in ("A", "C32") else 4)
     s.set_tuning(vk.Tuning(queries_per_block=args.queries_per_block, vectors_per_step=args.ilp,
                            blocks_per_query=args.blocks_per_query))
     dq = vk.DeviceArray.from_host(queries)

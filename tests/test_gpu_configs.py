@@ -6,7 +6,7 @@ ids identical and distance bits identical.
 Workloads (d = 128 throughout):
   A    100k vectors, m16, nq=100, k=10, Q=2            all queries
   B    1M, m16, nq=1000, k=10, Q=4 (the headline)      all queries; the launch shape is asserted
-  C32  1M, m32, nq=1000, k=100                         all queries
+  C32  1M, m32, nq=1000, k=100, Q=2 and Q=4           all queries
   C64  1M, m64, nq=1000, k=100                         all queries
   D    10M, m16, nq=1000, k=10                         the GPU searches all 1000, the first 100 are compared
   D1   10M, m16, nq=1, k=10                            the single-query search (one slab over every block)
@@ -112,7 +112,7 @@ def test_config_b_headline_all_queries_and_launch_shape():
         assert shape.blocks_x == 500
 
 
-@pytest.mark.parametrize("cfg,q", [("C32", 4), ("C64", 2)])
+@pytest.mark.parametrize("cfg,q", [("C32", 2), ("C32", 4), ("C64", 2)])
 def test_config_c_k100_all_queries(cfg, q):
     _, shape = run_config(cfg, q, 1000)
     assert shape.queries_per_block == q
