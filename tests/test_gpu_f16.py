@@ -154,8 +154,9 @@ def test_f16_tiny_database_and_nq_one():
 
 @pytest.mark.parametrize("family", ["random", "tie"])
 def test_f16_single_query_over_many_blocks(family):
-    # one query spread over ~37 blocks: each block appends only its entries at or below the slab's published bound,
-    # and the last block merges those candidates; repeated searches check that the slab state starts fresh
+    # one query spread over ~37 blocks: the last block bounds the k-th best by the k-th smallest head of the blocks'
+    # lists and merges only the pairs at or below it (tie-heavy data: pairs equal to the bound must survive);
+    # repeated searches check that the slab state starts fresh
     gen = datagen.random_fixture if family == "random" else datagen.tie_fixture
     n, d, m, nq = 300_007, 32, 16, 2
     centroids, codes, queries = gen(n, d, m, nq, seed=41)

@@ -143,8 +143,10 @@ def test_single_query_final_merge_paths(family):
 def test_final_merge_bound_equal_to_the_kth_best(variant):
     # The k best vectors each head a different block's list, so the bound (the k-th smallest head) is the k-th best
     # itself and exactly k pairs survive the filter: the pair equal to the bound must be kept. The 16 planted
-    # vectors have first code bytes 16 apart (one per block of the sorted layout, whose blocks cover a few first-byte
-    # values each) and distances 0.05^2 .. 0.8^2, far below the random vectors' (~60).
+    # vectors have first code bytes 16 apart and distances 0.05^2 .. 0.8^2, far below the random vectors' (~60).
+    # With 64 and 100 blocks they fall in 16 different blocks of the sorted, tile-spread layout (checked on the CPU
+    # against slot_order.hpp for this data); the default spread (37 blocks) puts two in one block and is kept as an
+    # ordinary parity case.
     rng = np.random.default_rng(17)
     n, d, m = 300_007, 32, 16
     centroids = rng.standard_normal((m, 256, d // m)).astype(np.float32)
@@ -159,7 +161,7 @@ def test_final_merge_bound_equal_to_the_kth_best(variant):
         codes[v, 1:] = 255
     oracle_search = orc.adc_search_f16 if variant == vk.ScanVariant.FusedWarpF16 else orc.adc_search
     with vk.PQSearcher(centroids, codes, d) as s:
-        for bpq in (0, 100):
+        for bpq in (0, 64, 100):
             s.set_tuning(vk.Tuning(queries_per_block=1, blocks_per_query=bpq))
             for k in (10, 16):
                 exp = oracle_search(centroids, d, codes, query, k)
@@ -221,6 +223,20 @@ def test_tiny_database_and_k_equal_n():
         for k in (1, 64, 70):
             got_d, got_i, _ = s.search(queries, k, vk.ScanVariant.FusedWarp)
             assert_same(got_d, got_i, orc.adc_search(centroids, d, codes, queries, k), f"n=70 k={k}")
+
+
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 768, 769, 4_160])
+def test_layout_block_boundaries(n):
+    # The sorted layout deals and spreads only full 256-slot blocks; a partial last block keeps its slots at the end,
+    # and padding slots up to the next 256 are never read as vectors. Sizes around those boundaries, every k kind.
+    d, m, nq = 32, 16, 3
+    centroids, codes, queries = datagen.random_fixture(n, d, m, nq, seed=n)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        for k in sorted({1, min(10, n), n if n <= 128 else 128}):
+            got_d, got_i, _ = s.search(queries, k, vk.ScanVariant.FusedWarp)
+            assert_same(got_d, got_i, orc.adc_search(centroids, d, codes, queries, k), f"v8 n={n} k={k}")
+            got_d, got_i, _ = s.search(queries, k, vk.ScanVariant.FusedWarpF16)
+            assert_same(got_d, got_i, orc.adc_search_f16(centroids, d, codes, queries, k), f"v9 n={n} k={k}")
 
 
 def test_device_resident_entry_point(fixture, searcher):
