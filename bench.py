@@ -253,6 +253,8 @@ def main():
                          "tables; 4 otherwise)")
     ap.add_argument("--ilp", type=int, default=4)
     ap.add_argument("--blocks-per-query", type=int, default=0)
+    ap.add_argument("--threads", type=int, default=0,
+                    help="v8/v9 block size: 512 or 1024 (0: the library chooses)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and its parity check")
     ap.add_argument("--no-recall", action="store_true", help="skip the exact ground truth and recall")
     ap.add_argument("--ivf-lists", type=int, default=0, metavar="NLIST",
@@ -299,8 +301,8 @@ def main():
     # at 2 (measured: m=32 2.05 ms at Q=2 against 2.18 at Q=4, the 64 KB tables leaving room for two blocks per CU)
     if args.queries_per_block is None:
         args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config in ("A", "C32") else 4)
-    s.set_tuning(vk.Tuning(queries_per_block=args.queries_per_block, vectors_per_step=args.ilp,
-                           blocks_per_query=args.blocks_per_query))
+    s.set_tuning(vk.Tuning(scan_threads=args.threads or 256, queries_per_block=args.queries_per_block,
+                           vectors_per_step=args.ilp, blocks_per_query=args.blocks_per_query))
     dq = vk.DeviceArray.from_host(queries)
     dout = vk.DeviceArray(nq * k * 8)
     for _ in range(args.warmup):

@@ -121,6 +121,27 @@ CASE("ivecs and bvecs readers") {
     EXPECT_THROWS(read_fvecs("does_not_exist.fvecs", n, d));
 }
 
+CASE("malformed vector files are rejected") {
+    const std::string path = "veckern_host_bad.fvecs";
+    auto write_words = [&](const std::vector<int32_t>& words, std::size_t extra_bytes) {
+        std::ofstream out(path, std::ios::binary);
+        out.write(reinterpret_cast<const char*>(words.data()), static_cast<std::streamsize>(4 * words.size()));
+        for (std::size_t i = 0; i < extra_bytes; ++i) out.put('\0');
+    };
+    std::size_t n = 0, d = 0;
+    write_words({}, 0);  // empty: no header
+    EXPECT_THROWS(read_fvecs(path, n, d));
+    write_words({0}, 0);  // dimension 0
+    EXPECT_THROWS(read_fvecs(path, n, d));
+    write_words({2, 0, 0, 2, 0, 0}, 2);  // two rows of d=2 and a truncated third
+    EXPECT_THROWS(read_fvecs(path, n, d));
+    write_words({2, 0, 0, 1, 0, 0}, 0);  // the second row claims d=1 though the size fits two rows of d=2
+    EXPECT_THROWS(read_fvecs(path, n, d));
+    const auto first = read_fvecs(path, n, d, 1);  // the first row alone is well formed
+    EXPECT(n == 1 && d == 2 && first.size() == 2);
+    std::remove(path.c_str());
+}
+
 CASE("exact search finds itself; the selector pads and orders by (dist, id)") {
     const std::size_t n = 4000, d = 32, k = 10;
     const auto base = synthetic_clustered(n, d, 20, 7);

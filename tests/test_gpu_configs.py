@@ -93,6 +93,7 @@ def run_config(cfg, q, compared, variant=vk.ScanVariant.FusedWarp, check_device=
     else:
         exp = cpu_search(w.centroids, w.codes, sample, w.k, w.d)
     assert_identical(dist[:compared], ids[:compared], exp, f"{cfg} {vk.variant_name(variant)} Q={q}")
+    w.dist, w.ids = dist, ids
     return w, shape
 
 
@@ -104,12 +105,21 @@ def test_config_a_all_queries():
 def test_config_b_headline_all_queries_and_launch_shape():
     w, shape = run_config("B", 4, 1000)
     info = vk.device_info()
-    assert shape.threads == 512 and shape.queries_per_block == 4 and shape.vectors_per_step == 4
-    # 250 slabs of 4 queries; with R resident blocks (occupancy x CUs) every slab gets floor(R / 250) of them.
-    resident = shape.blocks_per_sm * info.sm_count
-    assert shape.blocks_x == 250 * (resident // 250), (shape.blocks_x, resident)
-    if info.sm_count == 256 and shape.blocks_per_sm == 2:
-        assert shape.blocks_x == 500
+    # One 1024-thread block per CU (16 waves sharing one granule counter): 250 slabs of 4 queries, one block each
+    # while the slabs are no more than the CUs.
+    assert shape.threads == 1024 and shape.queries_per_block == 4 and shape.vectors_per_step == 4
+    assert shape.blocks_per_sm == 1
+    assert shape.blocks_x == 250 * max(1, info.sm_count // 250), (shape.blocks_x, info.sm_count)
+    # The 512-thread instances (two blocks per CU, each slab split between two blocks) return the same bits.
+    print("    [configs] B: GPU search with 512-thread blocks", flush=True)
+    with vk.PQSearcher(w.centroids, w.codes, w.d) as s:
+        s.set_tuning(vk.Tuning(scan_threads=512, queries_per_block=4))
+        dist, ids, _ = s.search(w.queries, w.k, vk.ScanVariant.FusedWarp)
+        narrow = s.last_launch()
+    assert narrow.threads == 512
+    resident = narrow.blocks_per_sm * info.sm_count
+    assert narrow.blocks_x == 250 * (resident // 250), (narrow.blocks_x, resident)
+    assert (ids == w.ids).all() and (dist.view(np.uint32) == w.dist.view(np.uint32)).all()
 
 
 @pytest.mark.parametrize("cfg,q", [("C32", 2), ("C32", 4), ("C64", 2)])

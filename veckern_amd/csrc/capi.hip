@@ -24,29 +24,29 @@
 
 namespace vk {
 // Per-m instance tables of the wave-list scan, fp32 (fused_wave_m*.hip) and fp16 tables (fused_wave_h*.hip).
-WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_m64(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_h16(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_h32(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_h64(int qg, int ng, int ilp, int segments, bool bulk);
-WaveScanKernel fused_wave_kernel_hx(int qg, int ng, int ilp, int segments, bool bulk);
+WaveScanKernel fused_wave_kernel_m16(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_m32(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_m64(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_mx(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_h16(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_h32(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_h64(int qg, int ng, int ilp, int segments, bool bulk, int threads);
+WaveScanKernel fused_wave_kernel_hx(int qg, int ng, int ilp, int segments, bool bulk, int threads);
 
-WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16, bool bulk) {
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16, bool bulk, int threads) {
     if (f16) {
         switch (m) {
-            case 16: return fused_wave_kernel_h16(qg, ng, ilp, segments, bulk);
-            case 32: return fused_wave_kernel_h32(qg, ng, ilp, segments, bulk);
-            case 64: return fused_wave_kernel_h64(qg, ng, ilp, segments, bulk);
-            default: return fused_wave_kernel_hx(qg, ng, ilp, segments, bulk);
+            case 16: return fused_wave_kernel_h16(qg, ng, ilp, segments, bulk, threads);
+            case 32: return fused_wave_kernel_h32(qg, ng, ilp, segments, bulk, threads);
+            case 64: return fused_wave_kernel_h64(qg, ng, ilp, segments, bulk, threads);
+            default: return fused_wave_kernel_hx(qg, ng, ilp, segments, bulk, threads);
         }
     }
     switch (m) {
-        case 16: return fused_wave_kernel_m16(qg, ng, ilp, segments, bulk);
-        case 32: return fused_wave_kernel_m32(qg, ng, ilp, segments, bulk);
-        case 64: return fused_wave_kernel_m64(qg, ng, ilp, segments, bulk);
-        default: return fused_wave_kernel_mx(qg, ng, ilp, segments, bulk);
+        case 16: return fused_wave_kernel_m16(qg, ng, ilp, segments, bulk, threads);
+        case 32: return fused_wave_kernel_m32(qg, ng, ilp, segments, bulk, threads);
+        case 64: return fused_wave_kernel_m64(qg, ng, ilp, segments, bulk, threads);
+        default: return fused_wave_kernel_mx(qg, ng, ilp, segments, bulk, threads);
     }
 }
 }  // namespace vk
@@ -335,20 +335,41 @@ struct vk_searcher {
         const size_t tables = static_cast<size_t>(w.q) * m * vk::KSUB * entry_bytes;
         require(tables <= info.max_smem_per_block, "LUT does not fit in LDS");
         w.smem = w.kern.dynamic_lds ? tables : 0;  // fixed-m instances hold the tables in static LDS
-        if (w.kern.dynamic_lds)
-            VK_HIP(hipFuncSetAttribute(w.kern.fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(w.smem)));
-        VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&w.per_cu, w.kern.fn, w.kern.threads, w.smem));
-        w.per_cu = std::max(w.per_cu, 1);
-
-        w.part = vk::plan::balanced_partition(static_cast<int64_t>(n), b, w.q, w.ilp,
-                                              static_cast<int64_t>(w.per_cu) * info.sm_count,
-                                              tuning.blocks_per_query, info.sm_count);
+        auto plan_for = [&](const vk::WaveScanKernel& k) {
+            if (k.dynamic_lds)
+                VK_HIP(hipFuncSetAttribute(k.fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(w.smem)));
+            VK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&w.per_cu, k.fn, k.threads, w.smem));
+            w.per_cu = std::max(w.per_cu, 1);
+            w.part = vk::plan::balanced_partition(static_cast<int64_t>(n), b, w.q, w.ilp,
+                                                  static_cast<int64_t>(w.per_cu) * info.sm_count,
+                                                  tuning.blocks_per_query, info.sm_count);
+        };
+        plan_for(w.kern);
+        // 1024-thread blocks where that instance exists and its blocks scan many vectors of their slabs (above the
+        // bulk-scan bound; and not crossing slab boundaries where 512-thread blocks would not): one block per CU,
+        // whose 16 waves share one granule counter, instead of two 512-thread blocks that the CU does not balance
+        // or one of 8 waves. scan_threads = 512 or 1024 pins the block size.
+        if (tuning.scan_threads != 512) {
+            const vk::WaveScanKernel wide =
+                vk::fused_wave_kernel(qg, ng, w.ilp, static_cast<int>(m), segments, f16, false, 1024);
+            if (wide.fn) {
+                const vk::WaveScanKernel narrow = w.kern;
+                const bool narrow_aligned = w.part.slabs <= static_cast<int64_t>(w.per_cu) * info.sm_count;
+                w.kern = wide;
+                plan_for(w.kern);
+                const bool crossing = w.part.slabs > static_cast<int64_t>(w.per_cu) * info.sm_count;
+                if (tuning.scan_threads != 1024 &&
+                    ((crossing && narrow_aligned) || vk::plan::bulk_scan(w.part, w.ilp))) {
+                    w.kern = narrow;
+                    plan_for(w.kern);
+                }
+            }
+        }
         // Few vectors per block: the instance that admits candidates in bulk, if it has the same residency (the
         // partition above was planned with it).
         if (!f16 && segments == 1 && w.q > 1 && vk::plan::bulk_scan(w.part, w.ilp)) {
             const vk::WaveScanKernel bulk = vk::fused_wave_kernel(qg, ng, w.ilp, static_cast<int>(m), segments, f16,
-                                                                  true);
+                                                                  true, w.kern.threads);
             int bulk_per_cu = 0;
             if (bulk.fn) {
                 if (bulk.dynamic_lds)

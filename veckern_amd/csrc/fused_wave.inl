@@ -170,7 +170,38 @@ __device__ __forceinline__ uint32_t scaled_byte(uint32_t w, int b) {
     return r;
 }
 
+// Byte B of w times 2^SHIFT written into the low half of r, whose high half is kept (SDWA dst_sel:WORD_0 with
+// dst_unused:UNUSED_PRESERVE). A DS instruction's immediate offset reaches 64 KB; with r's high half at 1, r is the
+// byte's table offset plus 64 KB in one VALU op, so tables past 64 KB of LDS cost no extra add per lookup. The
+// scaled byte (at most 255 << 4) fits the 16-bit half.
+template <int SHIFT, int B>
+__device__ __forceinline__ void scaled_byte_low_half(uint32_t& r, uint32_t w) {
+    static_assert(B >= 0 && B < 4 && (255 << SHIFT) < 65536, "byte select and 16-bit result");
+    const uint32_t shift = SHIFT;
+    if constexpr (B == 0)
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_0"
+            : "+v"(r) : "v"(shift), "v"(w));
+    else if constexpr (B == 1)
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_1"
+            : "+v"(r) : "v"(shift), "v"(w));
+    else if constexpr (B == 2)
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_2"
+            : "+v"(r) : "v"(shift), "v"(w));
+    else
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_3"
+            : "+v"(r) : "v"(shift), "v"(w));
+}
+
 constexpr int log2_int(int x) { return x <= 1 ? 0 : 1 + log2_int(x / 2); }
+
+// Compile-time unrolled loop: f(std::integral_constant<int, I>) for I = 0 .. N-1.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 
 // Loads n consecutive floats from p (16-byte aligned when n % 4 == 0, 8-byte aligned when n == 2) with the widest
 // vector loads the alignment allows.
@@ -266,26 +297,30 @@ __device__ __forceinline__ void table_entries(const WaveScanArgs& a, const float
     else table_entries_w<QS, M, W, 0>(a, qrow, wave, lane, sink);
 }
 
-// Writes the NG query-interleaved tables of a slab into LDS (`tables`, NG tables of table_bytes each). fp16 tables
-// take each query's power-of-two shift from the per-query maxima in `qmax` (raw fp32 bits).
+// Writes the NG query-interleaved tables of a slab into LDS, interleaved per sub-space: group t's entries of
+// sub-space s are the 256 entries at ((s * NG + t) * 256 + c) * entry bytes, so the NG reads of one code byte lie
+// within 256 * NG entries of each other and share one address register (immediate offsets). fp16 tables take each
+// query's power-of-two shift from the per-query maxima in `qmax` (raw fp32 bits).
 template <int QG, int NG, int M, int W, bool F16>
 __device__ __forceinline__ void build_tables(const WaveScanArgs& a, const float* const (&qrow)[QG * NG],
-                                             unsigned char* tables, int table_bytes, const unsigned* qmax, int wave,
-                                             int lane) {
+                                             unsigned char* tables, const unsigned* qmax, int wave, int lane) {
     constexpr int QS = QG * NG;
     constexpr int EB = Entries<QG, F16>::kBytes;
     if constexpr (!F16) {
-        auto sink = [&](int s, int c, const float* acc) {
+        // One group of QG queries at a time: the unrolled pass holds QG query rows and their sums, not QS.
+#pragma unroll 1
+        for (int t = 0; t < NG; ++t) {
+            const float* group[QG];
 #pragma unroll
-            for (int t = 0; t < NG; ++t) {
-                unsigned char* dst = tables + t * table_bytes + (s * KSUB + c) * EB;
-                if constexpr (QG == 4) *reinterpret_cast<float4*>(dst) = make_float4(acc[t * 4], acc[t * 4 + 1],
-                                                                                     acc[t * 4 + 2], acc[t * 4 + 3]);
-                else if constexpr (QG == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc[t * 2], acc[t * 2 + 1]);
-                else *reinterpret_cast<float*>(dst) = acc[t];
-            }
-        };
-        table_entries<QS, M, W>(a, qrow, wave, lane, sink);
+            for (int q = 0; q < QG; ++q) group[q] = qrow[t * QG + q];
+            auto sink = [&](int s, int c, const float* acc) {
+                unsigned char* dst = tables + ((s * NG + t) * KSUB + c) * EB;
+                if constexpr (QG == 4) *reinterpret_cast<float4*>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                else if constexpr (QG == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc[0], acc[1]);
+                else *reinterpret_cast<float*>(dst) = acc[0];
+            };
+            table_entries<QG, M, W>(a, group, wave, lane, sink);
+        }
     } else {
         int shift[QS];
 #pragma unroll
@@ -296,7 +331,7 @@ __device__ __forceinline__ void build_tables(const WaveScanArgs& a, const float*
             for (int q = 0; q < QS; ++q) h[q] = to_half_bits(ldexpf(acc[q], -shift[q]));
 #pragma unroll
             for (int t = 0; t < NG; ++t) {
-                unsigned char* dst = tables + t * table_bytes + (s * KSUB + c) * EB;
+                unsigned char* dst = tables + ((s * NG + t) * KSUB + c) * EB;
                 const uint32_t* g = h + t * QG;
                 if constexpr (QG == 8)
                     *reinterpret_cast<uint4*>(dst) = make_uint4(g[0] | g[1] << 16, g[2] | g[3] << 16,
@@ -447,6 +482,9 @@ __device__ bool merge_query_filtered(const Pair* first, int lists, int K, int k,
     }
     __syncthreads();
     const unsigned survivors = *count;
+    // Every thread holds the count before any wave writes `buf` again: the fallback merge stores wave lists over
+    // the bounds and the count, and a wave still to read the count would otherwise take the other branch.
+    __syncthreads();
     if (survivors > static_cast<unsigned>(cap)) return false;  // block-uniform: every thread read the same count
     if (wave == 0) {
         if (survivors <= static_cast<unsigned>(WAVE)) {
@@ -489,6 +527,7 @@ __device__ __forceinline__ void merge_query(const Pair* first, int lists, int K,
 // tiles (a granule's tiles start at a multiple of U, and U <= 4).
 template <int U>
 struct SlotIds {
+    static_assert(U == 1 || U == 2 || U == 4, "a granule's tiles lie within one group of four tiles");
     uint32_t w[U];
     __device__ __forceinline__ void load(const uint32_t* slot_ids, int64_t tile0, int lane) {
         const uint32_t* p = slot_ids + (tile0 >> 2) * 256 + lane * 4 + (tile0 & 3);
@@ -575,7 +614,7 @@ __global__ void __launch_bounds__(T)
     // When every (query, wave) slot fits in one wave, a step reads all of them with one LDS read (lane l: slot l)
     // and takes each query's maximum over its W lanes by DPP exchanges; a wave publishes its QS values with one
     // LDS write (lane q: query q), always (they only fall).
-    constexpr bool kLaneBound = kShareBound && QS * W <= WAVE && (W == 2 || W == 4 || W == 8);
+    constexpr bool kLaneBound = kShareBound && QS * W <= WAVE && (W == 2 || W == 4 || W == 8 || W == 16);
     __shared__ __align__(16) unsigned rank_bound[QS][W];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
@@ -592,6 +631,12 @@ __global__ void __launch_bounds__(T)
     if (IVF && b >= grid) return;  // block-uniform, before any barrier
     const int64_t start = b * total / grid, end = (b + 1) * total / grid;
     const _Float16 one = opaque_half_one();
+    // Address registers of the sub-spaces whose tables lie past the first 64 KB of LDS: the high half stays 1, the
+    // low half takes each lookup's scaled code byte (scaled_byte_low_half).
+    constexpr bool kWindowed = M > 0 && NG * M * KSUB * E::kBytes > 65536;
+    uint32_t hi[kWindowed ? 16 : 1];
+#pragma unroll
+    for (int j = 0; j < (kWindowed ? 16 : 1); ++j) hi[j] = 0x10000u;
 
     // Inverted lists: the first slab of the block's range by binary search (the last slab starting at or before
     // `start`, i.e. the non-empty one holding it); every later one is the next non-empty slab, so the search costs
@@ -680,7 +725,7 @@ __global__ void __launch_bounds__(T)
                 __syncthreads();
             }
             if constexpr (IVF) gather_tables<QG, M, T>(a, lrow, tables, tid);
-            else build_tables<QG, NG, M, W, F16>(a, qrow, tables, table_bytes, qmax, wave, lane);
+            else build_tables<QG, NG, M, W, F16>(a, qrow, tables, qmax, wave, lane);
             if constexpr (kShareBound)
                 for (int t = tid; t < QS * W; t += T) (&rank_bound[0][0])[t] = 0x7f800000u;  // +inf
             if (!IVF && tid == 0) next_gran = W;
@@ -766,28 +811,52 @@ __global__ void __launch_bounds__(T)
                 // 16 lookups of one code word, sub-spaces 16w .. 16w+15 in order; the first sub-space of a vector
                 // (w == 0 with m fixed) sets the accumulators instead of adding to zeroed ones.
                 constexpr int kShift = log2_int(E::kBytes);
-                auto lookup_word = [&](const uint4 word, const int w) {
+                // Entry group t of code byte j of a word: its LDS address is reg + imm (imm a compile-time
+                // immediate offset below 64 KB). With m fixed, sub-space s's groups start at s * NG * 256 entries;
+                // those past 64 KB take their byte offset in a register whose high half is 1 (hi[j]), the rest
+                // the plain scaled byte. WC: the word index, a compile-time constant when m is fixed.
+                auto address = [&](const uint32_t (&part)[4], auto jc, auto wc, uint32_t& reg, int& imm) {
+                    constexpr int j = decltype(jc)::value;
+                    if constexpr (M > 0) {
+                        constexpr int base = (decltype(wc)::value * 16 + j) * NG * KSUB * E::kBytes;
+                        static_assert((base >> 16) <= 1 && ((base + NG * KSUB * E::kBytes - 1) >> 16) == (base >> 16),
+                                      "a sub-space's entry groups lie in one 64 KB window, the first or the second");
+                        if constexpr ((base >> 16) == 0) {
+                            reg = scaled_byte<kShift>(part[j >> 2], j & 3);
+                            imm = base;
+                        } else {
+                            scaled_byte_low_half<kShift, j & 3>(hi[j], part[j >> 2]);
+                            reg = hi[j];
+                            imm = base - 65536;
+                        }
+                    } else {
+                        reg = scaled_byte<kShift>(part[j >> 2], j & 3);
+                        imm = (static_cast<int>(wc) * 16 + j) * NG * KSUB * E::kBytes;
+                    }
+                };
+                auto lookup_word = [&](const uint4 word, auto wc) {
                     const uint32_t part[4] = {word.x, word.y, word.z, word.w};
-                    const bool first = M > 0 && w == 0;
+                    bool first = false;
+                    if constexpr (M > 0) first = decltype(wc)::value == 0;
                     if constexpr (F16 && QG >= 4) {
                         // The word's reads are issued eight at a time before their accumulations: the
                         // one-statement-per-read accumulations would otherwise be scheduled right behind their own
                         // read, one read in flight at a time. Eight, not all sixteen: the sixteen results held 64
                         // VGPRs and made the 8-query loop reload spilled values every step (8 queries: 1M -0.8 %,
                         // 10M -1.4 %).
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
+                        static_for<0, 2>([&](auto hc) {
+                            constexpr int h = decltype(hc)::value;
                             V v[8 * NG];
-#pragma unroll
-                            for (int jj = 0; jj < 8; ++jj) {
-                                const int j = h * 8 + jj;
-                                const uint32_t off = scaled_byte<kShift>(part[j >> 2], j & 3);
-                                const int s = w * 16 + j;
+                            static_for<0, 8>([&](auto jjc) {
+                                constexpr int jj = decltype(jjc)::value;
+                                uint32_t reg;
+                                int imm;
+                                address(part, std::integral_constant<int, h * 8 + jj>{}, wc, reg, imm);
 #pragma unroll
                                 for (int t = 0; t < NG; ++t)
-                                    v[jj * NG + t] = *reinterpret_cast<const V*>(
-                                        tables + t * table_bytes + s * KSUB * E::kBytes + off);
-                            }
+                                    v[jj * NG + t] =
+                                        *reinterpret_cast<const V*>(tables + reg + imm + t * KSUB * E::kBytes);
+                            });
                             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                             for (int jj = 0; jj < 8; ++jj)
@@ -796,34 +865,55 @@ __global__ void __launch_bounds__(T)
                                     if (first && h == 0 && jj == 0) E::set(&acc[t * QG], v[jj * NG + t]);
                                     else E::add(&acc[t * QG], v[jj * NG + t], one);
                                 }
-                        }
+                        });
                         return;
                     }
+                    // The reads are issued in batches of 16 (16 / NG sub-spaces), each batch before its adds: 16
+                    // reads in flight per wave, in 64 VGPRs at most (four-query entries). Left to itself the scheduler
+                    // either hoists every read of a tile (eight queries: 128 VGPRs, spilled) or, with the sums fenced
+                    // before the offers, waits for each read before issuing the next.
+                    constexpr int kBatch = 16 / NG;
+                    static_for<0, 16 / kBatch>([&](auto bc) {
+                        constexpr int b = decltype(bc)::value;
+                        V v[kBatch * NG];
+                        static_for<0, kBatch>([&](auto jjc) {
+                            constexpr int jj = decltype(jjc)::value;
+                            uint32_t reg;
+                            int imm;
+                            address(part, std::integral_constant<int, b * kBatch + jj>{}, wc, reg, imm);
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const uint32_t off = scaled_byte<kShift>(part[j >> 2], j & 3);
-                        const int s = w * 16 + j;
+                            for (int t = 0; t < NG; ++t)
+                                v[jj * NG + t] =
+                                    *reinterpret_cast<const V*>(tables + reg + imm + t * KSUB * E::kBytes);
+                        });
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int t = 0; t < NG; ++t) {
-                            const V v = *reinterpret_cast<const V*>(tables + t * table_bytes + s * KSUB * E::kBytes +
-                                                                    off);
-                            if (first && j == 0) E::set(&acc[t * QG], v);
-                            else E::add(&acc[t * QG], v, one);
-                        }
-                    }
+                        for (int jj = 0; jj < kBatch; ++jj)
+#pragma unroll
+                            for (int t = 0; t < NG; ++t) {
+                                if (first && b == 0 && jj == 0) E::set(&acc[t * QG], v[jj * NG + t]);
+                                else E::add(&acc[t * QG], v[jj * NG + t], one);
+                            }
+                        __builtin_amdgcn_sched_barrier(0);
+                    });
                 };
                 if constexpr (M > 0) {
-#pragma unroll
-                    for (int w = 0; w < WORDS; ++w) lookup_word(cw[u][w], w);
+                    static_for<0, WORDS>([&](auto wc) { lookup_word(cw[u][decltype(wc)::value], wc); });
                 } else {
                     for (int w = 0; w < words; ++w) lookup_word(tile_codes[(u * words + w) * WAVE], w);
                 }
+                // Every query's sum is complete here, before the first offer: left alone, the compiler sinks each
+                // query's adds to just before that query's offer, so the table reads of the later queries stay live
+                // across the earlier queries' insert branches (eight queries: spilled to scratch).
+#pragma unroll
+                for (int q = 0; q < QS; ++q) asm volatile("" : "+v"(acc[q]));
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (kLaneBound) {
                     if (u == 0) {  // raw bits of distances >= 0 or +inf: signed order is float order
                         int mx = max(bound_raw, xor_lane<1>(bound_raw));
                         if constexpr (W > 2) mx = max(mx, xor_lane<2>(mx));
                         if constexpr (W > 4) mx = max(mx, xor_lane<4>(mx));
+                        if constexpr (W > 8) mx = max(mx, xor_lane<8>(mx));
 #pragma unroll
                         for (int q = 0; q < QS; ++q)
                             lists[q].set_cap(__int_as_float(__builtin_amdgcn_readlane(mx, q * W)));
@@ -903,6 +993,19 @@ __global__ void __launch_bounds__(T)
         const int slots = a.max_slots;  // every slab reserves max_slots blocks
         Pair* const slab_part = a.part + slab * QS * a.max_slots * lpb * static_cast<int64_t>(a.K);
         Pair* const buf = reinterpret_cast<Pair*>(tables);  // QS * W * K pairs fit in the tables' space
+        if (count == 1) {
+            // The block scanned the whole slab: its wave lists go to LDS and wave q merges query q's W lists
+            // straight into the results, with no partial lists in HBM, no fences and no ticket.
+            __syncthreads();  // every wave has finished reading the tables
+#pragma unroll
+            for (int q = 0; q < QS; ++q) lists[q].store(buf + (q * W + wave) * a.K, a.K);
+            __syncthreads();
+            for (int q = wave; q < QS && slab * QS + q < a.nq; q += W)
+                merge_query_wave<S>(buf + q * W * a.K, W, a.K, a.k, a.out + (slab * QS + q) * a.k,
+                                    F16 ? table_shift(qmax[q]) : 0, lane);
+            item = slab_next;
+            continue;
+        }
         if (lpb == 1) {
             __syncthreads();  // every wave has finished reading the tables
 #pragma unroll
@@ -959,9 +1062,8 @@ hipError_t launch_fused_wave_t(const WaveScanArgs& a, int grid, size_t smem, hip
     return hipGetLastError();
 }
 
-template <int QG, int NG, int U, int M, int S, bool F16, bool IVF = false, bool BULK = false>
+template <int QG, int NG, int U, int M, int S, bool F16, bool IVF = false, bool BULK = false, int T = 512>
 WaveScanKernel make_wave_kernel() {
-    constexpr int T = 512;
     WaveScanKernel k;
     k.fn = reinterpret_cast<const void*>(&fused_wave_kernel_t<QG, NG, U, M, S, T, F16, IVF, BULK>);
     k.threads = T;
@@ -969,6 +1071,15 @@ WaveScanKernel make_wave_kernel() {
     k.launch = &launch_fused_wave_t<QG, NG, U, M, S, T, F16, IVF, BULK>;
     return k;
 }
+
+// 1024-thread blocks (16 waves, 128 VGPRs each): one block holds all of a CU's waves and its LDS granule counter
+// balances them. Where the tables leave room for two 512-thread blocks per CU, those two are not balanced: the older
+// block's waves get issue priority, so on every CU one block ended its scan ~30 % before the other, which then ran
+// alone at half occupancy (1M x nq=1000: 590 against 770 us; 10M: 4.4 against 5.9 ms). Where the tables take more
+// than half the LDS, 512 threads are 8 waves per CU. The block merge of 16 wave lists per query must fit the tables'
+// space (QS * 16 * 64S pairs).
+template <int QG, int NG, int M, int S, bool F16>
+constexpr bool kWideBlock = M > 0 && QG * NG * 16 * WAVE * S * 8 <= NG * M * KSUB * Entries<QG, F16>::kBytes;
 
 // Inverted-list instances for one M: fp32 tables, one query per slab, four tiles per wave step (each list is
 // padded to a multiple of 256 vectors).
@@ -982,27 +1093,32 @@ WaveScanKernel select_ivf_kernel(int segments) {
 // Instances for one M and entry type: every (QG, NG) whose tables fit in 160 KB of LDS when M is known. fp32
 // tables: QG 1, 2, 4 and two groups of 4; fp16 tables: QG 1, 2, 4, 8 in one group. `bulk` asks for bulk admission
 // into one-register lists: a second instance of the fp32 multi-query kernels (the others admit in bulk already, or,
-// fp16, never); an empty result when there is none.
+// fp16, never). threads: 512, or 1024 where kWideBlock holds (four tiles per wave step only). An empty result when
+// there is no such instance.
 template <int M, bool F16>
-WaveScanKernel select_wave_kernel(int qg, int ng, int ilp, int segments, bool bulk) {
+WaveScanKernel select_wave_kernel(int qg, int ng, int ilp, int segments, bool bulk, int threads) {
     constexpr int kLds = 160 * 1024;
+#define VK_WAVE_ILP(QG_, NG_, S_, BULK_)                                                                    \
+    if (threads == 1024) {                                                                                 \
+        if constexpr (kWideBlock<QG_, NG_, M, S_, F16>) {                                                  \
+            if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, S_, F16, false, BULK_, 1024>();          \
+        }                                                                                                  \
+        return WaveScanKernel{};                                                                           \
+    }                                                                                                      \
+    if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, S_, F16, false, BULK_>();                        \
+    if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, S_, F16, false, BULK_>();                        \
+    if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, S_, F16, false, BULK_>();
 #define VK_WAVE_CASE(QG_, NG_)                                                                      \
     if (qg == QG_ && ng == NG_) {                                                                   \
         if constexpr (M == 0 || NG_ * M * KSUB * Entries<QG_, F16>::kBytes <= kLds) {               \
             if (segments == 1 && bulk) {                                                            \
                 if constexpr (!F16 && QG_ * NG_ > 1) {                                              \
-                    if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 1, F16, false, true>();   \
-                    if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 1, F16, false, true>();   \
-                    if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 1, F16, false, true>();   \
+                    VK_WAVE_ILP(QG_, NG_, 1, true)                                                  \
                 }                                                                                   \
             } else if (segments == 1) {                                                             \
-                if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 1, F16>();                    \
-                if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 1, F16>();                    \
-                if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 1, F16>();                    \
+                VK_WAVE_ILP(QG_, NG_, 1, false)                                                     \
             } else if (segments == 2) {                                                             \
-                if (ilp == 1) return make_wave_kernel<QG_, NG_, 1, M, 2, F16>();                    \
-                if (ilp == 2) return make_wave_kernel<QG_, NG_, 2, M, 2, F16>();                    \
-                if (ilp == 4) return make_wave_kernel<QG_, NG_, 4, M, 2, F16>();                    \
+                VK_WAVE_ILP(QG_, NG_, 2, false)                                                     \
             }                                                                                       \
         }                                                                                           \
         return WaveScanKernel{};                                                                    \
@@ -1019,6 +1135,7 @@ WaveScanKernel select_wave_kernel(int qg, int ng, int ilp, int segments, bool bu
         VK_WAVE_CASE(8, 1)
     }
 #undef VK_WAVE_CASE
+#undef VK_WAVE_ILP
     return WaveScanKernel{};
 }
 

@@ -1,8 +1,17 @@
 // Vector-file readers and seeded synthetic data (reference interface: include/veckern/io.hpp, src/cpu/io.cpp).
 #include "veckern/io.hpp"
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cerrno>
 #include <cmath>
-#include <fstream>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
 
 #include "philox.hpp"
 #include "veckern/common.hpp"
@@ -10,56 +19,105 @@
 namespace veckern {
 namespace {
 
-template <typename T>
-std::vector<T> read_rows(const std::string& path, std::size_t& n, std::size_t& d, std::size_t max_n) {
-    std::ifstream in(path, std::ios::binary);
-    check(in.good(), "cannot open " + path);
-    int32_t dim = 0;
-    in.read(reinterpret_cast<char*>(&dim), sizeof(dim));
-    check(in.good() && dim > 0, "bad header in " + path);
-    in.seekg(0, std::ios::end);
-    const auto bytes = static_cast<std::size_t>(in.tellg());
-    const std::size_t row = sizeof(int32_t) + sizeof(T) * static_cast<std::size_t>(dim);
-    check(bytes % row == 0, "file size is not a multiple of the row size: " + path);
-    n = bytes / row;
-    if (max_n > 0 && max_n < n) n = max_n;
-    d = static_cast<std::size_t>(dim);
-    std::vector<T> out(n * d);
-    in.seekg(0);
-    for (std::size_t i = 0; i < n; ++i) {
-        int32_t row_dim = 0;
-        in.read(reinterpret_cast<char*>(&row_dim), sizeof(row_dim));
-        check(row_dim == dim, "inconsistent dimension in " + path);
-        in.read(reinterpret_cast<char*>(out.data() + i * d), static_cast<std::streamsize>(sizeof(T) * d));
+// The whole file as one read-only mapping (no stream state, no per-row reads); unmapped when it goes out of scope.
+class FileView {
+public:
+    explicit FileView(const std::string& path) {
+        const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+        if (fd < 0) throw std::runtime_error(path + ": " + std::strerror(errno));
+        struct stat st {};
+        const bool sized = ::fstat(fd, &st) == 0;
+        size_ = sized ? static_cast<std::size_t>(st.st_size) : 0;
+        if (sized && size_ > 0) {
+            void* p = ::mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd, 0);
+            if (p != MAP_FAILED) base_ = static_cast<const unsigned char*>(p);
+        }
+        ::close(fd);
+        if (!sized || (size_ > 0 && !base_)) throw std::runtime_error(path + ": the file cannot be mapped");
     }
-    check(in.good(), "truncated file " + path);
+    ~FileView() {
+        if (base_) ::munmap(const_cast<unsigned char*>(base_), size_);
+    }
+    FileView(const FileView&) = delete;
+    FileView& operator=(const FileView&) = delete;
+    const unsigned char* data() const { return base_; }
+    std::size_t size() const { return size_; }
+
+private:
+    const unsigned char* base_ = nullptr;
+    std::size_t size_ = 0;
+};
+
+int32_t le_int32(const unsigned char* p) {  // the files are little-endian, like the host
+    int32_t v;
+    std::memcpy(&v, p, sizeof(v));
+    return v;
+}
+
+// Rows of the *vecs formats: each row is an int32 count d followed by d values of type T, every row with the same
+// d. The row count follows from the file size, which must be a whole number of rows; at most max_n rows (0: all)
+// are returned, row-major, and each returned row's own count is checked against the first.
+template <typename T>
+std::vector<T> load_rows(const std::string& path, std::size_t& n, std::size_t& d, std::size_t max_n) {
+    const FileView file(path);
+    if (file.size() < sizeof(int32_t)) throw std::runtime_error(path + ": no row header (file too short)");
+    const int32_t dim = le_int32(file.data());
+    if (dim <= 0) throw std::runtime_error(path + ": row header gives dimension " + std::to_string(dim));
+    const std::size_t stride = sizeof(int32_t) + sizeof(T) * static_cast<std::size_t>(dim);
+    if (file.size() % stride != 0)
+        throw std::runtime_error(path + ": " + std::to_string(file.size()) + " bytes are not whole rows of " +
+                                 std::to_string(stride) + " bytes (dimension " + std::to_string(dim) + ")");
+    const std::size_t rows = file.size() / stride;
+    const std::size_t take = max_n > 0 ? std::min(rows, max_n) : rows;
+    std::vector<T> out(take * static_cast<std::size_t>(dim));
+    long long bad_row = -1;  // the first row whose count differs, if any
+#pragma omp parallel for schedule(static) reduction(max : bad_row)
+    for (long long r = 0; r < static_cast<long long>(take); ++r) {
+        const unsigned char* row = file.data() + static_cast<std::size_t>(r) * stride;
+        if (le_int32(row) != dim) {
+            bad_row = std::max(bad_row, r);
+            continue;
+        }
+        std::memcpy(out.data() + static_cast<std::size_t>(r) * dim, row + sizeof(int32_t), stride - sizeof(int32_t));
+    }
+    if (bad_row >= 0)
+        throw std::runtime_error(path + ": row " + std::to_string(bad_row) + " does not have dimension " +
+                                 std::to_string(dim));
+    n = take;
+    d = static_cast<std::size_t>(dim);
     return out;
 }
 
 }  // namespace
 
 std::vector<float> read_fvecs(const std::string& path, std::size_t& n, std::size_t& d, std::size_t max_n) {
-    return read_rows<float>(path, n, d, max_n);
+    return load_rows<float>(path, n, d, max_n);
 }
 
 std::vector<float> read_bvecs(const std::string& path, std::size_t& n, std::size_t& d, std::size_t max_n) {
-    const auto bytes = read_rows<uint8_t>(path, n, d, max_n);
-    return std::vector<float>(bytes.begin(), bytes.end());
+    const std::vector<uint8_t> bytes = load_rows<uint8_t>(path, n, d, max_n);
+    std::vector<float> out(bytes.size());
+    std::transform(bytes.begin(), bytes.end(), out.begin(), [](uint8_t b) { return static_cast<float>(b); });
+    return out;
 }
 
 std::vector<int32_t> read_ivecs(const std::string& path, std::size_t& n, std::size_t& d, std::size_t max_n) {
-    return read_rows<int32_t>(path, n, d, max_n);
+    return load_rows<int32_t>(path, n, d, max_n);
 }
 
+// One buffer per file: every row's header and values are laid out in memory, then written with a single call.
 void write_fvecs(const std::string& path, const float* x, std::size_t n, std::size_t d) {
-    std::ofstream out(path, std::ios::binary);
-    check(out.good(), "cannot create " + path);
+    const std::size_t stride = sizeof(int32_t) + sizeof(float) * d;
+    std::vector<unsigned char> buf(n * stride);
     const int32_t dim = static_cast<int32_t>(d);
     for (std::size_t i = 0; i < n; ++i) {
-        out.write(reinterpret_cast<const char*>(&dim), sizeof(dim));
-        out.write(reinterpret_cast<const char*>(x + i * d), static_cast<std::streamsize>(sizeof(float) * d));
+        std::memcpy(buf.data() + i * stride, &dim, sizeof(dim));
+        std::memcpy(buf.data() + i * stride + sizeof(dim), x + i * d, sizeof(float) * d);
     }
-    check(out.good(), "write failed: " + path);
+    std::FILE* f = std::fopen(path.c_str(), "wb");
+    if (!f) throw std::runtime_error(path + ": " + std::strerror(errno));
+    const bool ok = std::fwrite(buf.data(), 1, buf.size(), f) == buf.size();
+    if (std::fclose(f) != 0 || !ok) throw std::runtime_error(path + ": write failed");
 }
 
 // ---------------------------------------------------------------- Gaussian mixture

@@ -69,8 +69,10 @@ struct WaveScanKernel {
 };
 
 // Returns a kernel with fn == nullptr when the combination is not built. f16: binary16 tables (v9). bulk: the
-// instance with bulk admission into one-register lists (fp32, more than one query per block only).
-WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16, bool bulk = false);
+// instance with bulk admission into one-register lists (fp32, more than one query per block only). threads: block
+// size, 512 or 1024 (built for four tiles per wave step where two 512-thread blocks' tables fit one CU).
+WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, bool f16, bool bulk = false,
+                                 int threads = 512);
 // The inverted-list scan (ivf_m*.hip): fp32 tables, one query per slab, four tiles per wave step.
 WaveScanKernel ivf_kernel(int m, int segments);
 
