@@ -150,7 +150,9 @@ int vk_search_device(vk_searcher* s, const float* d_queries, size_t nq, size_t k
                      vk_timings* timings);
 
 /* Allocation-free device-resident search. No counterpart in the reference: it is for callers that cannot allocate
- * device memory during a search (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * device memory during a search (tight serving loops, harnesses that forbid hipMalloc). It launches on the
+ * searcher's own stream and waits for that stream before returning, so it cannot be recorded into a caller's HIP
+ * graph.
  * Same arguments, results and errors as vk_search_device for v8_fused_warp and v9_fused_warp_f16 (other variants:
  * VK_ERR_INVALID_ARGUMENT), but the partial lists and slab counters live in a static device array of
  * VK_NOALLOC_SCRATCH_BYTES that the library holds on each device it runs on until the process ends (the first
