@@ -132,6 +132,13 @@ int vk_searcher_set_tuning(vk_searcher* s, const vk_tuning* t);
 int vk_searcher_get_tuning(const vk_searcher* s, vk_tuning* out);
 /* gpu.hpp:74 last_launch. */
 int vk_searcher_last_launch(const vk_searcher* s, vk_launch_shape* out);
+/* The slot order of the v8/v9 code layout: out[count] receives, for each slot of the searcher's n padded to a
+ * multiple of 256 (count must be that padded size), the id of the vector scanned there, interleaved by four 64-slot
+ * tiles (out[(tile / 4) * 256 + lane * 4 + tile % 4] for slot = tile * 64 + lane; padding slots hold 0). Built on
+ * the GPU on the first call or v8/v9 search. No counterpart in the reference (whose layouts keep vector order);
+ * for tests and tools that inspect the layout. Errors: m % 16 != 0 or count != padded n (VK_ERR_INVALID_ARGUMENT).
+ */
+int vk_searcher_slot_ids(vk_searcher* s, uint32_t* out, size_t count);
 
 /* gpu.hpp:61 search (searcher.cu:466-520): out[nq * k] host memory, ascending (dist, id) per query, padded
  * {+inf, -1}. Errors: k not in [1, min(128, n)] (VK_ERR_RUNTIME), m % 16 != 0 for v2/v6/v7/v8 or tables that

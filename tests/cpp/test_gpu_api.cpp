@@ -6,6 +6,8 @@
 #include <vector>
 
 #include "check.hpp"
+#include "slot_order.hpp"
+#include "veckern/veckern.h"
 #include "veckern/gpu.hpp"
 #include "veckern/io.hpp"
 #include "veckern/pq.hpp"
@@ -254,4 +256,28 @@ CASE("IVFSearcher probing every list equals the exhaustive search; fewer lists m
     ivf.search(f.queries.data(), f.nq, 5, k, got.data());
     same(got, expected, "ivf nprobe 5");
     EXPECT_THROWS(ivf.search(f.queries.data(), f.nq, nlist + 1, k, got.data()));
+}
+
+CASE("the slot order built on the GPU equals the host's (sort, dealing, tile spread, interleave)") {
+    struct Case {
+        std::size_t n, m;
+        bool uniform;  // uniform random codes (blocks dealt) or the fixture's clustered codes (m = 16)
+    };
+    const Case cases[] = {{50'003, 16, true}, {50'003, 16, false}, {20'000, 32, true}, {9'999, 64, true},
+                          {100, 16, true}, {768, 16, true}, {70'000, 48, true}};
+    for (const Case& c : cases) {
+        std::vector<uint8_t> codes(c.n * c.m);
+        if (c.uniform) uniform_codes(0, c.n, c.m, 5 + c.m, codes.data());
+        else codes.assign(fixture().codes.begin(), fixture().codes.begin() + c.n * c.m);
+        const std::size_t d = c.m * 2, n_pad = (c.n + 255) / 256 * 256;
+        const std::vector<float> centroids(c.m * 256 * 2, 0.5f);
+        vk_searcher* s = nullptr;
+        EXPECT(vk_searcher_create(centroids.data(), d, c.m, codes.data(), c.n, &s) == VK_OK);
+        std::vector<uint32_t> gpu_ids(n_pad, 0xdeadbeefu);
+        EXPECT(vk_searcher_slot_ids(s, gpu_ids.data(), n_pad) == VK_OK);
+        EXPECT(vk_searcher_slot_ids(s, gpu_ids.data(), n_pad + 1) == VK_ERR_INVALID_ARGUMENT);
+        vk_searcher_destroy(s);
+        const std::vector<uint32_t> host_ids = vk::order::slot_ids(codes.data(), c.n, c.m, n_pad, 4);
+        EXPECT(gpu_ids == host_ids);
+    }
 }

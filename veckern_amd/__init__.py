@@ -106,6 +106,7 @@ _SIGNATURES = {
     "vk_searcher_set_tuning": (ctypes.c_int, [_P, ctypes.POINTER(_Tuning)]),
     "vk_searcher_get_tuning": (ctypes.c_int, [_P, ctypes.POINTER(_Tuning)]),
     "vk_searcher_last_launch": (ctypes.c_int, [_P, ctypes.POINTER(_LaunchShape)]),
+    "vk_searcher_slot_ids": (ctypes.c_int, [_P, _P, ctypes.c_size_t]),
     "vk_search": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P,
                                  ctypes.POINTER(_Timings)]),
     "vk_distances": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P, ctypes.POINTER(_Timings)]),
@@ -310,6 +311,13 @@ class PQSearcher:
         c = _Tuning()
         _check(library().vk_searcher_get_tuning(self._h, ctypes.byref(c)))
         return Tuning(c.scan_threads, c.blocks_per_query, c.queries_per_block, c.vectors_per_step)
+
+    def slot_ids(self) -> np.ndarray:
+        """The v8/v9 layout's slot order: per slot of n padded to 256, the id of the vector scanned there,
+        interleaved by four tiles (vk_searcher_slot_ids)."""
+        out = np.empty((self.n + 255) // 256 * 256, dtype=np.uint32)
+        _check(library().vk_searcher_slot_ids(self._h, out.ctypes.data, out.size))
+        return out
 
     def last_launch(self) -> LaunchShape:
         s = _LaunchShape()

@@ -263,7 +263,7 @@ struct vk_searcher {
     DeviceBuffer<unsigned> counters;
     size_t counters_zeroed = 0;
     bool counters_dirty = false;
-    bool have_il = false, have_v = false, have_s = false;
+    bool have_il = false, have_v = false, have_s = false, have_slot_ids = false;
     std::unique_ptr<StageClock> clock_pool;
 
     ~vk_searcher() {
@@ -292,12 +292,37 @@ struct vk_searcher {
             have_v = built = true;
         }
         if (vk::plan::uses_sorted_layout(v) && !have_s) {
+            ensure_slot_ids();
             codes_s.ensure(static_cast<size_t>(n_pad) * (m / 16));
             VK_HIP(vk::launch_build_sorted_words(codes.get(), n, static_cast<int>(m), n_pad, slot_ids.get(),
                                                  codes_s.get(), stream));
             have_s = built = true;
         }
         if (built) VK_HIP(hipStreamSynchronize(stream));  // a layout kernel's failure surfaces here, not mid-search
+    }
+
+    // The slot order of the fused scans' layout (slot_order.hip, the order of slot_order.hpp), built on the GPU the
+    // first time a v8/v9 search (or vk_searcher_slot_ids) needs it; its scratch is freed right after.
+    void ensure_slot_ids() {
+        if (have_slot_ids) return;
+        require(m % 16 == 0, "the sorted code layout needs m % 16 == 0");
+        slot_ids.ensure(static_cast<size_t>(n_pad));
+        if (m > 64) {  // beyond the GPU kernel's LDS sizing: the same order computed on the host
+            std::vector<uint8_t> host_codes(n * m);
+            VK_HIP(hipMemcpy(host_codes.data(), codes.get(), n * m, hipMemcpyDeviceToHost));
+            const std::vector<uint32_t> order = vk::order::slot_ids(host_codes.data(), n, m, static_cast<size_t>(n_pad));
+            VK_HIP(hipMemcpy(slot_ids.get(), order.data(), order.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+            have_slot_ids = true;
+            return;
+        }
+        size_t bytes = 0;
+        VK_HIP(vk::slot_order_scratch_bytes(static_cast<int64_t>(n), &bytes));
+        DeviceBuffer<unsigned char> scratch;
+        scratch.ensure(bytes);
+        VK_HIP(vk::launch_slot_order(codes.get(), static_cast<int64_t>(n), static_cast<int>(m), n_pad, scratch.get(),
+                                     bytes, slot_ids.get(), stream));
+        VK_HIP(hipStreamSynchronize(stream));
+        have_slot_ids = true;
     }
 
     // The stage clock of this searcher's calls: its events are created once and reused by every call.
@@ -828,11 +853,6 @@ VK_EXPORT int vk_searcher_create(const float* centroids, size_t d, size_t m, con
         VK_HIP(hipMemcpy(s->centroids.get(), centroids, m * vk::KSUB * (d / m) * sizeof(float), hipMemcpyHostToDevice));
         s->codes.ensure(n * m);
         VK_HIP(hipMemcpy(s->codes.get(), codes, n * m, hipMemcpyHostToDevice));
-        if (m % 16 == 0) {  // the slot order of the fused scans' layout (slot_order.hpp)
-            const std::vector<uint32_t> order = vk::order::slot_ids(codes, n, m, static_cast<size_t>(s->n_pad));
-            s->slot_ids.ensure(order.size());
-            VK_HIP(hipMemcpy(s->slot_ids.get(), order.data(), order.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
-        }
         *out = s.release();
     });
 }
@@ -859,6 +879,18 @@ VK_EXPORT int vk_searcher_last_launch(const vk_searcher* s, vk_launch_shape* out
     return guarded([&] {
         require(s != nullptr && out != nullptr, "null argument");
         *out = s->last;
+    });
+}
+
+VK_EXPORT int vk_searcher_slot_ids(vk_searcher* s, uint32_t* out, size_t count) {
+    return guarded([&] {
+        require(s != nullptr && out != nullptr, "null argument");
+        if (count != static_cast<size_t>(s->n_pad))
+            fail(VK_ERR_INVALID_ARGUMENT, "count must be n rounded up to a multiple of 256");
+        if (s->m % 16 != 0) fail(VK_ERR_INVALID_ARGUMENT, "the sorted layout needs m % 16 == 0");
+        s->use_device();
+        s->ensure_slot_ids();
+        VK_HIP(hipMemcpy(out, s->slot_ids.get(), count * sizeof(uint32_t), hipMemcpyDeviceToHost));
     });
 }
 

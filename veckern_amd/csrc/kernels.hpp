@@ -27,6 +27,11 @@ hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_
                               hipStream_t stream);
 // Zeroes count 32-bit words with a kernel (no memset node).
 hipError_t launch_zero_words(unsigned* p, int64_t count, hipStream_t stream);
+// The fused scans' slot order on the GPU (slot_order.hip), equal to order::slot_ids of slot_order.hpp: `out` receives
+// n_pad interleaved slot ids (padding slots 0). scratch: slot_order_scratch_bytes(n) bytes of device memory.
+hipError_t slot_order_scratch_bytes(int64_t n, size_t* bytes);
+hipError_t launch_slot_order(const uint8_t* codes, int64_t n, int m, int64_t n_pad, void* scratch,
+                             size_t scratch_bytes, uint32_t* out, hipStream_t stream);
 
 // ---- fused scan with wave-cooperative lists (fused_wave_*.hip)
 struct WaveScanArgs {

@@ -50,7 +50,7 @@ __global__ void __launch_bounds__(256)
         uint4 v = make_uint4(0, 0, 0, 0);
         if (slot < n) {
             const int64_t i = slot_ids[(tile >> 2) * 256 + lane * 4 + (tile & 3)];
-            v = *reinterpret_cast<const uint4*>(codes + (i * words + w) * 16);
+            if (i < n) v = *reinterpret_cast<const uint4*>(codes + (i * words + w) * 16);  // ids are < n
         }
         out[o] = v;
     }

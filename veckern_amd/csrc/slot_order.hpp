@@ -1,4 +1,6 @@
-// Slot order of the fused scans' code layout (host side, at searcher creation while the codes are at hand).
+// Slot order of the fused scans' code layout: the host definition. Searchers build the same order on the GPU
+// (slot_order.hip, checked slot for slot against this one) the first time a v8/v9 search needs it; this host
+// version orders inverted-list members at index build and the layouts of m > 64.
 //
 // A wave64 ds_read_b128 is served in four passes of 16 consecutive lanes; within a pass, lanes reading different
 // 16-byte table entries of one bank group (entry index mod 16, 64 banks of 4 bytes) queue one behind another, and
