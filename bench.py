@@ -306,10 +306,11 @@ def main():
     t_setup = time.perf_counter()
     s = vk.PQSearcher(centroids, codes, d)
     setup_s = time.perf_counter() - t_setup
-    # Queries per block: fp16 tables put 8 queries in one 16-byte table read; 100k and 1M at m=32 (k=100) run faster
-    # at 2 (measured: m=32 2.05 ms at Q=2 against 2.18 at Q=4, the 64 KB tables leaving room for two blocks per CU)
+    # Queries per block: fp16 tables put 8 queries in one 16-byte table read; 100k runs faster at 2 (launch- and
+    # latency-bound: more, smaller slabs); 1M at m=32 (k=100) at 4 with one 1024-thread block per CU (1.86 ms against
+    # 1.92 at Q=2); m=64 at 2, the most its tables allow.
     if args.queries_per_block is None:
-        args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config in ("A", "C32") else 4)
+        args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config == "A" else 4)
     s.set_tuning(vk.Tuning(scan_threads=args.threads or 256, queries_per_block=args.queries_per_block,
                            vectors_per_step=args.ilp, blocks_per_query=args.blocks_per_query))
     dq = vk.DeviceArray.from_host(queries)

@@ -33,11 +33,12 @@ __device__ __forceinline__ float lane_read(float v, int lane) {
 }
 __device__ __forceinline__ int32_t lane_read(int32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
-// DPP wave_shr:1 — lane l receives lane l-1's value (lane 0 keeps its own). One VALU op, no LDS traffic.
+// DPP wave_shr:1 — lane l receives lane l-1's value; lane 0 receives 0 (bound_ctrl). One VALU op, no LDS traffic and
+// no copy of the destination's old value.
 __device__ __forceinline__ float wave_shr1(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x138, 0xf, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x138, 0xf, 0xf, true));
 }
-__device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgcn_update_dpp(v, v, 0x138, 0xf, 0xf, false); }
+__device__ __forceinline__ int32_t wave_shr1(int32_t v) { return __builtin_amdgcn_mov_dpp(v, 0x138, 0xf, 0xf, true); }
 
 // The value of lane ^ J. Within a row of 16 lanes by DPP (VALU only): quad_perm for J = 1, 2; for J = 4, 8 a
 // row_shl:J into the lanes whose bit J is clear and a row_shr:J into the others, selected by bank (4-lane group)
@@ -118,7 +119,8 @@ __device__ __forceinline__ void wave_clean(uint64_t& k) {
 // `cap` is an optional outside bound: the threshold of another list over a disjoint part of the same candidate
 // stream (a sibling wave's). A candidate farther than it has K better candidates in that list, so it cannot be in
 // the merged top K and is not offered; ties at the cap are still offered, which keeps the (dist, id) order exact.
-template <int S, bool BULK = (S > 1)>
+// CAP = false: the list never takes an outside bound (set_cap is not called), so its filter is its threshold.
+template <int S, bool BULK = (S > 1), bool CAP = true>
 struct WaveList {
     float d[S];
     int32_t id[S];
@@ -146,6 +148,7 @@ struct WaveList {
     }
 
     __device__ __forceinline__ void set_cap(float c) {
+        static_assert(CAP, "a list built without an outside bound");
         cap = c;
         filter = fminf(thr_d, cap);
     }
@@ -197,7 +200,7 @@ struct WaveList {
             thr_d = lane_read(d[S - 1], t - (S - 1) * WAVE);
             thr_i = lane_read(id[S - 1], t - (S - 1) * WAVE);
         }
-        filter = fminf(thr_d, cap);
+        filter = CAP ? fminf(thr_d, cap) : thr_d;
     }
 
     // Each lane offers one candidate. The ballot uses dist <= threshold as a cheap superset test. A few admitted

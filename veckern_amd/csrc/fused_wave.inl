@@ -632,11 +632,13 @@ __global__ void __launch_bounds__(T)
     const int64_t start = b * total / grid, end = (b + 1) * total / grid;
     const _Float16 one = opaque_half_one();
     // Address registers of the sub-spaces whose tables lie past the first 64 KB of LDS: the high half stays 1, the
-    // low half takes each lookup's scaled code byte (scaled_byte_low_half).
+    // low half takes each lookup's scaled code byte (scaled_byte_low_half). A few registers in rotation: a read
+    // takes its address when it issues, so the register is free for the fourth lookup after it.
     constexpr bool kWindowed = M > 0 && NG * M * KSUB * E::kBytes > 65536;
-    uint32_t hi[kWindowed ? 16 : 1];
+    constexpr int kHi = kWindowed ? 4 : 1;
+    uint32_t hi[kHi];
 #pragma unroll
-    for (int j = 0; j < (kWindowed ? 16 : 1); ++j) hi[j] = 0x10000u;
+    for (int j = 0; j < kHi; ++j) hi[j] = 0x10000u;
 
     // Inverted lists: the first slab of the block's range by binary search (the last slab starting at or before
     // `start`, i.e. the non-empty one holding it); every later one is the next non-empty slab, so the search costs
@@ -650,7 +652,7 @@ __global__ void __launch_bounds__(T)
     // costs about 1 %. The fp16 kernels (Q = 8) have no registers to spare for it in the loop. Lists that admit
     // one by one still take a wave's first granule step in bulk (kPeel, at the scan loop).
     constexpr bool kBulkOne = QS == 1 && !F16;
-    WaveList<S, IVF || (!F16 && S > 1) || kBulkOne || BULK> lists[QS];
+    WaveList<S, IVF || (!F16 && S > 1) || kBulkOne || BULK, kShareBound> lists[QS];
     float published[QS];
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
     int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
@@ -825,8 +827,8 @@ __global__ void __launch_bounds__(T)
                             reg = scaled_byte<kShift>(part[j >> 2], j & 3);
                             imm = base;
                         } else {
-                            scaled_byte_low_half<kShift, j & 3>(hi[j], part[j >> 2]);
-                            reg = hi[j];
+                            scaled_byte_low_half<kShift, j & 3>(hi[j % kHi], part[j >> 2]);
+                            reg = hi[j % kHi];
                             imm = base - 65536;
                         }
                     } else {
