@@ -309,8 +309,11 @@ def main():
     # Queries per block: fp16 tables put 8 queries in one 16-byte table read; 100k runs faster at 2 (launch- and
     # latency-bound: more, smaller slabs); 1M at m=32 (k=100) at 4 with one 1024-thread block per CU (1.86 ms against
     # 1.92 at Q=2); m=64 at 2, the most its tables allow.
+    # 10M (nq=1000) at 8: the search is VALU-bound there and eight queries share each code byte's address op (5.30
+    # against 5.40 ms at Q=4); at 1M eight queries per block cost more in per-block tables and merges than they save.
     if args.queries_per_block is None:
-        args.queries_per_block = 8 if variant == vk.ScanVariant.FusedWarpF16 else (2 if args.config == "A" else 4)
+        args.queries_per_block = (8 if variant == vk.ScanVariant.FusedWarpF16 or args.config == "D"
+                                  else (2 if args.config == "A" else 4))
     s.set_tuning(vk.Tuning(scan_threads=args.threads or 256, queries_per_block=args.queries_per_block,
                            vectors_per_step=args.ilp, blocks_per_query=args.blocks_per_query))
     dq = vk.DeviceArray.from_host(queries)
