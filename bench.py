@@ -237,12 +237,13 @@ def bench_ivf(args, centroids, codes, queries, base):
     print(json.dumps(record), flush=True)
 
 
-def load_traffic(cfg):
-    """HBM bytes per scan launch measured with rocprofv3 --pmc (profiles/traffic.json), if recorded."""
+def load_traffic(cfg, f16):
+    """Counter record of the search kernel for this configuration (profiles/traffic.json, from rocprofv3 --pmc runs):
+    HBM bytes per launch and the binding pipe, if recorded."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(cfg)
+            return json.load(f).get(cfg + ("/v9" if f16 else ""))
     except (OSError, ValueError):
         return None
 
@@ -357,17 +358,20 @@ def main():
     q_eff = shape.queries_per_block
     hbm_bytes = float(n) * m * math.ceil(nq / q_eff)
     f16 = variant == vk.ScanVariant.FusedWarpF16
-    # The binding pipe, from the counters of this kernel (SQ_INSTS_VALU per CU-cycle; LDS-active CU-cycles): the
-    # VALU issues 0.90 (1M) to 0.99 (10M) wave64 instructions per CU-cycle against one possible, at 5.2-5.8 VALU
-    # instructions per 16-byte table read, while the LDS is 75-89 % busy; fp16 tables: the VALU as well.
+    # The binding pipe, from the counters of this kernel (profiles/traffic.json): "valu" where the VALU issues more
+    # wave64 instructions per CU-cycle than the LDS is busy (1M and 10M at m=16: 0.91-0.93 against 77-90 %; fp16
+    # tables), "lds" where bank conflicts keep the LDS busier (m=32 and m=64 at k=100, 100M uniform codes: 87-97 %).
+    counters = load_traffic(args.config, f16) or {}
     roofline = {
-        "bound": "valu",
+        "bound": counters.get("bound", "valu"),
+        "bound_basis": ({"valu_instr_per_cu_cycle": counters["valu_per_cu_cycle"], "lds_busy": counters["lds_busy"]}
+                        if "lds_busy" in counters else None),
         "achieved": achieved / 1e12,
         "peak": peak / 1e12,
         "unit": "Tlookup/s",
         "frac": achieved / peak,
-        "traffic": (load_traffic(args.config) or {}).get("bytes_per_launch"),
-        "traffic_detail": load_traffic(args.config),
+        "traffic": counters.get("bytes_per_launch"),
+        "traffic_detail": counters or None,
         "kernel": "fused_wave_kernel_t (scan + per-wave top-k)",
         "kernel_ms": scan_ms,
         "algorithmic": f"n*m*nq = {lookups:.3e} LDS lookups per launch (one {2 if f16 else 4}-byte table read + "
