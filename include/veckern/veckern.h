@@ -132,13 +132,17 @@ int vk_searcher_set_tuning(vk_searcher* s, const vk_tuning* t);
 int vk_searcher_get_tuning(const vk_searcher* s, vk_tuning* out);
 /* gpu.hpp:74 last_launch. */
 int vk_searcher_last_launch(const vk_searcher* s, vk_launch_shape* out);
-/* The slot order of the v8/v9 code layout: out[count] receives, for each slot of the searcher's n padded to a
- * multiple of 256 (count must be that padded size), the id of the vector scanned there, interleaved by four 64-slot
- * tiles (out[(tile / 4) * 256 + lane * 4 + tile % 4] for slot = tile * 64 + lane; padding slots hold 0). Built on
- * the GPU on the first call or v8/v9 search. No counterpart in the reference (whose layouts keep vector order);
- * for tests and tools that inspect the layout. Errors: m % 16 != 0 or count != padded n (VK_ERR_INVALID_ARGUMENT).
- */
-int vk_searcher_slot_ids(vk_searcher* s, uint32_t* out, size_t count);
+/* The v8/v9 code layout. ids[ids_count] receives, for each slot of the searcher's n padded to a multiple of 256
+ * (ids_count must be that padded size), the id of the vector scanned there, interleaved by four 64-slot tiles
+ * (ids[(tile / 4) * 256 + lane * 4 + tile % 4] for slot = tile * 64 + lane; padding slots hold 0). rows[rows_count]
+ * (rows_count must be m * 256; rows may be NULL with rows_count 0) receives the LDS table row of each code value
+ * (rows[s * 256 + c]): the layout stores rows in place of codes and the scan writes the entry of code c at row
+ * rows[s * 256 + c]. *lanes (may be NULL) receives the lanes per table-read pass the layout was built for: the
+ * first v8/v9 search builds it for its own reads (16 for 16-byte entries, 32 for 8-byte, 64 for 4-byte), a call
+ * before any such search for 16. Built on the GPU. No counterpart in the reference (whose layouts keep vector order
+ * and codes); for tests and tools that inspect the layout. Errors: m % 16 != 0 or a count that does not match
+ * (VK_ERR_INVALID_ARGUMENT). */
+int vk_searcher_layout(vk_searcher* s, uint32_t* ids, size_t ids_count, uint8_t* rows, size_t rows_count, int* lanes);
 
 /* gpu.hpp:61 search (searcher.cu:466-520): out[nq * k] host memory, ascending (dist, id) per query, padded
  * {+inf, -1}. Errors: k not in [1, min(128, n)] (VK_ERR_RUNTIME), m % 16 != 0 for v2/v6/v7/v8 or tables that

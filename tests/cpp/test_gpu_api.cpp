@@ -258,13 +258,15 @@ CASE("IVFSearcher probing every list equals the exhaustive search; fewer lists m
     EXPECT_THROWS(ivf.search(f.queries.data(), f.nq, nlist + 1, k, got.data()));
 }
 
-CASE("the slot order built on the GPU equals the host's (sort, dealing, tile spread, interleave)") {
+CASE("the code layout built on the GPU equals the host's (sort, row fit, dealing, tile spread, interleave)") {
     struct Case {
         std::size_t n, m;
         bool uniform;  // uniform random codes (blocks dealt) or the fixture's clustered codes (m = 16)
+        int q;         // queries per block of the search that builds the layout (0: none, built for 16 lanes)
     };
-    const Case cases[] = {{50'003, 16, true}, {50'003, 16, false}, {20'000, 32, true}, {9'999, 64, true},
-                          {100, 16, true}, {768, 16, true}, {70'000, 48, true}};
+    const Case cases[] = {{50'003, 16, true, 0},  {50'003, 16, false, 0}, {20'000, 32, true, 0}, {9'999, 64, true, 0},
+                          {100, 16, true, 0},     {768, 16, true, 0},     {70'000, 48, true, 0}, {50'003, 16, false, 2},
+                          {20'000, 64, true, 2},  {30'000, 16, false, 1}, {12'345, 32, true, 1}};
     for (const Case& c : cases) {
         std::vector<uint8_t> codes(c.n * c.m);
         if (c.uniform) uniform_codes(0, c.n, c.m, 5 + c.m, codes.data());
@@ -273,11 +275,26 @@ CASE("the slot order built on the GPU equals the host's (sort, dealing, tile spr
         const std::vector<float> centroids(c.m * 256 * 2, 0.5f);
         vk_searcher* s = nullptr;
         EXPECT(vk_searcher_create(centroids.data(), d, c.m, codes.data(), c.n, &s) == VK_OK);
+        const int lanes_expected = c.q == 0 ? 16 : c.q == 2 ? 32 : 64;
+        if (c.q) {
+            vk_tuning t{};
+            EXPECT(vk_searcher_get_tuning(s, &t) == VK_OK);
+            t.queries_per_block = c.q;
+            EXPECT(vk_searcher_set_tuning(s, &t) == VK_OK);
+            const std::vector<float> q(static_cast<std::size_t>(c.q) * d, 0.25f);
+            std::vector<vk_neighbor> out(static_cast<std::size_t>(c.q));
+            EXPECT(vk_search(s, q.data(), c.q, 1, VK_V8_FUSED_WARP, out.data(), nullptr) == VK_OK);
+        }
         std::vector<uint32_t> gpu_ids(n_pad, 0xdeadbeefu);
-        EXPECT(vk_searcher_slot_ids(s, gpu_ids.data(), n_pad) == VK_OK);
-        EXPECT(vk_searcher_slot_ids(s, gpu_ids.data(), n_pad + 1) == VK_ERR_INVALID_ARGUMENT);
+        std::vector<uint8_t> gpu_rows(c.m * 256, 0);
+        int lanes = 0;
+        EXPECT(vk_searcher_layout(s, gpu_ids.data(), n_pad, gpu_rows.data(), gpu_rows.size(), &lanes) == VK_OK);
+        EXPECT(lanes == lanes_expected);
+        EXPECT(vk_searcher_layout(s, gpu_ids.data(), n_pad + 1, nullptr, 0, nullptr) == VK_ERR_INVALID_ARGUMENT);
+        EXPECT(vk_searcher_layout(s, gpu_ids.data(), n_pad, gpu_rows.data(), 5, nullptr) == VK_ERR_INVALID_ARGUMENT);
         vk_searcher_destroy(s);
-        const std::vector<uint32_t> host_ids = vk::order::slot_ids(codes.data(), c.n, c.m, n_pad, 4);
-        EXPECT(gpu_ids == host_ids);
+        const vk::order::SlotOrder host = vk::order::slot_order(codes.data(), c.n, c.m, n_pad, lanes_expected, 4);
+        EXPECT(gpu_rows == host.rows);
+        EXPECT(gpu_ids == host.ids);
     }
 }

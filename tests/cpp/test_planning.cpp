@@ -156,26 +156,39 @@ std::vector<uint8_t> random_codes(size_t n, size_t m, uint64_t seed, int distinc
     return c;
 }
 
-// Mean over the full 256-slot blocks' (pass, sub-space) pairs of the largest number of distinct table entries in
-// one 16-byte bank group (entry % 16) among a pass's 16 lanes; vec_of(slot) gives the slot's vector.
+// Mean over the full 256-slot blocks' (pass, sub-space) pairs of the largest number of distinct table entries in one
+// bank group among a pass's `lanes` lanes, the group of code e of sub-space s being rows[s * 256 + e] % lanes
+// (rows empty: e % lanes); vec_of(slot) gives the slot's vector. Written out here, independently of
+// vk::order::block_stats.
 template <typename F>
-double bank_load(const std::vector<uint8_t>& codes, size_t n, size_t m, F vec_of) {
+double bank_load(const std::vector<uint8_t>& codes, size_t n, size_t m, int lanes, const std::vector<uint8_t>& rows,
+                 F vec_of) {
     double total = 0;
     size_t count = 0;
-    for (size_t p0 = 0; p0 + 16 <= n / 256 * 256; p0 += 16)
+    for (size_t p0 = 0; p0 + lanes <= n / 256 * 256; p0 += lanes)
         for (size_t s = 0; s < m; ++s) {
             bool seen[256] = {};
-            int groups[16] = {}, mx = 0;
-            for (size_t l = 0; l < 16; ++l) {
+            int groups[64] = {}, mx = 0;
+            for (int l = 0; l < lanes; ++l) {
                 const int e = codes[vec_of(p0 + l) * m + s];
                 if (seen[e]) continue;
                 seen[e] = true;
-                mx = std::max(mx, ++groups[e & 15]);
+                const int row = rows.empty() ? e : rows[s * 256 + e];
+                mx = std::max(mx, ++groups[row % lanes]);
             }
             total += mx;
             ++count;
         }
     return total / count;
+}
+
+bool is_permutation_of_rows(const std::vector<uint8_t>& rows, size_t m) {
+    for (size_t s = 0; s < m; ++s) {
+        std::vector<char> hit(256, 0);
+        for (int e = 0; e < 256; ++e) hit[rows[s * 256 + e]] = 1;
+        if (std::count(hit.begin(), hit.end(), 1) != 256) return false;
+    }
+    return true;
 }
 
 }  // namespace
@@ -184,49 +197,53 @@ CASE("slot order: slots [0, n) hold every vector once, blocks sorted by code byt
     const std::pair<size_t, size_t> shapes[] = {{1, 16},     {63, 16},         {300, 16},          {4096, 32},
                                                 {65536, 16}, {65536 + 700, 16}, {3 * 65536 + 17, 16}};
     for (const auto& [n, m] : shapes)
-        for (int clustered : {0, 5}) {
-            const std::vector<uint8_t> codes = random_codes(n, m, n * 7 + m + clustered, clustered);
-            const size_t n_pad = (n + 255) / 256 * 256;
-            const std::vector<uint32_t> ids = vk::order::slot_ids(codes.data(), n, m, n_pad, 1);
-            EXPECT(ids == vk::order::slot_ids(codes.data(), n, m, n_pad, 3));
-            EXPECT(ids.size() == n_pad);
-            std::vector<char> seen(n, 0);
-            bool once = true;
-            for (size_t slot = 0; slot < n; ++slot) {
-                const size_t v = ids[vk::order::interleaved(slot)];
-                once = once && v < n && !seen[v];
-                if (v < n) seen[v] = 1;
-            }
-            EXPECT(once);
-            // Sorted slot t sits at slot spread_slot(t): tiles of the full blocks spread, the partial block in place.
-            // Taken in sorted order block by block, every vector of a later block sorts at or after every vector of
-            // an earlier one (dealing only permutes within a block).
-            auto key = [&](size_t v) { return (uint32_t(codes[v * m]) << 24) | (uint32_t(codes[v * m + 1]) << 16) |
-                                              (uint32_t(codes[v * m + 2]) << 8) | codes[v * m + 3]; };
-            const size_t tiles = n / 256 * 4, stride = vk::order::spread_stride(tiles);
-            std::vector<char> used(n, 0);
-            bool bijective = true, sorted = true;
-            uint32_t prev_max = 0;
-            for (size_t b0 = 0; b0 < n; b0 += 256) {
-                uint32_t lo = UINT32_MAX, hi = 0;
-                for (size_t t = b0; t < std::min(n, b0 + 256); ++t) {
-                    const size_t at = vk::order::spread_slot(t, tiles, stride);
-                    bijective = bijective && at < n && !used[at];
-                    if (at >= n) continue;
-                    used[at] = 1;
-                    const uint32_t k = key(ids[vk::order::interleaved(at)]);
-                    lo = std::min(lo, k);
-                    hi = std::max(hi, k);
+        for (int clustered : {0, 5})
+            for (int lanes : {16, 32, 64}) {
+                if (lanes != 16 && n > 70000) continue;  // the wider passes on the smaller shapes
+                const std::vector<uint8_t> codes = random_codes(n, m, n * 7 + m + clustered, clustered);
+                const size_t n_pad = (n + 255) / 256 * 256;
+                const vk::order::SlotOrder o = vk::order::slot_order(codes.data(), n, m, n_pad, lanes, 1);
+                const std::vector<uint32_t>& ids = o.ids;
+                const vk::order::SlotOrder o3 = vk::order::slot_order(codes.data(), n, m, n_pad, lanes, 3);
+                EXPECT(ids == o3.ids && o.rows == o3.rows && o.lanes == lanes);
+                EXPECT(ids.size() == n_pad && o.rows.size() == m * 256 && is_permutation_of_rows(o.rows, m));
+                std::vector<char> seen(n, 0);
+                bool once = true;
+                for (size_t slot = 0; slot < n; ++slot) {
+                    const size_t v = ids[vk::order::interleaved(slot)];
+                    once = once && v < n && !seen[v];
+                    if (v < n) seen[v] = 1;
                 }
-                sorted = sorted && (b0 == 0 || prev_max <= lo);
-                prev_max = hi;
+                EXPECT(once);
+                // Sorted slot t sits at slot spread_slot(t): tiles of the full blocks spread, the partial block in
+                // place. Taken in sorted order block by block, every vector of a later block sorts at or after
+                // every vector of an earlier one (dealing only permutes within a block).
+                auto key = [&](size_t v) { return (uint32_t(codes[v * m]) << 24) | (uint32_t(codes[v * m + 1]) << 16) |
+                                                  (uint32_t(codes[v * m + 2]) << 8) | codes[v * m + 3]; };
+                const size_t tiles = n / 256 * 4, stride = vk::order::spread_stride(tiles);
+                std::vector<char> used(n, 0);
+                bool bijective = true, sorted = true;
+                uint32_t prev_max = 0;
+                for (size_t b0 = 0; b0 < n; b0 += 256) {
+                    uint32_t lo = UINT32_MAX, hi = 0;
+                    for (size_t t = b0; t < std::min(n, b0 + 256); ++t) {
+                        const size_t at = vk::order::spread_slot(t, tiles, stride);
+                        bijective = bijective && at < n && !used[at];
+                        if (at >= n) continue;
+                        used[at] = 1;
+                        const uint32_t k = key(ids[vk::order::interleaved(at)]);
+                        lo = std::min(lo, k);
+                        hi = std::max(hi, k);
+                    }
+                    sorted = sorted && (b0 == 0 || prev_max <= lo);
+                    prev_max = hi;
+                }
+                EXPECT(bijective);
+                EXPECT(sorted);
+                bool pad_zero = true;
+                for (size_t slot = n; slot < n_pad; ++slot) pad_zero = pad_zero && ids[vk::order::interleaved(slot)] == 0;
+                EXPECT(pad_zero);
             }
-            EXPECT(bijective);
-            EXPECT(sorted);
-            bool pad_zero = true;
-            for (size_t slot = n; slot < n_pad; ++slot) pad_zero = pad_zero && ids[vk::order::interleaved(slot)] == 0;
-            EXPECT(pad_zero);
-        }
 }
 
 CASE("slot order: the spread stride is coprime with the tile count and near its golden section") {
@@ -271,9 +288,95 @@ CASE("slot order: an inverted list's members sorted by code key (ties by id), fu
 CASE("slot order: the order lowers the LDS bank load of uniform random codes") {
     const size_t n = 2 * 65536, m = 16;
     const std::vector<uint8_t> codes = random_codes(n, m, 99);
-    const std::vector<uint32_t> ids = vk::order::slot_ids(codes.data(), n, m, n, 2);
-    const double natural = bank_load(codes, n, m, [](size_t slot) { return slot; });
-    const double ordered = bank_load(codes, n, m, [&](size_t slot) { return size_t{ids[vk::order::interleaved(slot)]}; });
-    std::printf("    bank load: vector order %.3f, slot order %.3f\n", natural, ordered);
-    EXPECT(natural > 2.8 && ordered < 2.3);
+    for (int lanes : {16, 32}) {
+        const vk::order::SlotOrder o = vk::order::slot_order(codes.data(), n, m, n, lanes, 2);
+        const double natural = bank_load(codes, n, m, lanes, {}, [](size_t slot) { return slot; });
+        const double ordered = bank_load(codes, n, m, lanes, o.rows,
+                                         [&](size_t slot) { return size_t{o.ids[vk::order::interleaved(slot)]}; });
+        std::printf("    %d lanes per pass: bank load in vector order %.3f, slot order %.3f\n", lanes, natural, ordered);
+        EXPECT(natural > (lanes == 16 ? 2.8 : 3.0) && ordered < natural * 0.8);
+    }
+}
+
+CASE("slot order: co-occurrence counts are symmetric, the GPU's upper triangle mirrors to them, and match a count") {
+    const size_t n = 20 * 256 + 9, m = 16;
+    const std::vector<uint8_t> codes = random_codes(n, m, 5, 40);
+    const std::vector<uint32_t> sorted = vk::order::sorted_ids(codes.data(), n, m, 1);
+    for (int lanes : {16, 64}) {
+        const std::vector<uint32_t> w = vk::order::cooccurrence(codes.data(), n, m, sorted.data(), lanes, 3);
+        std::vector<uint32_t> upper(w.size(), 0);
+        bool symmetric = true, zero_diagonal = true;
+        for (size_t s = 0; s < m; ++s)
+            for (int a = 0; a < 256; ++a) {
+                zero_diagonal = zero_diagonal && w[(s * 256 + a) * 256 + a] == 0;
+                for (int b = 0; b < 256; ++b) {
+                    symmetric = symmetric && w[(s * 256 + a) * 256 + b] == w[(s * 256 + b) * 256 + a];
+                    if (a < b) upper[(s * 256 + a) * 256 + b] = w[(s * 256 + a) * 256 + b];
+                }
+            }
+        EXPECT(symmetric && zero_diagonal);
+        vk::order::mirror_counts(upper, m);
+        EXPECT(upper == w);
+        // Every full block is sampled here (20 < kSampleBlocks): entry pairs counted directly, sub-space 3.
+        uint64_t pairs = 0, total = 0;
+        for (size_t b0 = 0; b0 + 256 <= n; b0 += 256)
+            for (size_t p0 = b0; p0 < b0 + 256; p0 += lanes) {
+                std::vector<int> distinct;
+                for (int l = 0; l < lanes; ++l) {
+                    const int e = codes[sorted[p0 + l] * m + 3];
+                    if (std::find(distinct.begin(), distinct.end(), e) == distinct.end()) distinct.push_back(e);
+                }
+                pairs += distinct.size() * (distinct.size() - 1);
+            }
+        for (int a = 0; a < 256; ++a)
+            for (int b = 0; b < 256; ++b) total += w[(3 * 256 + a) * 256 + b];
+        EXPECT(pairs == total);
+    }
+}
+
+CASE("slot order: fitted table rows put entries that are read together into different bank groups") {
+    // 16 cliques of 16 entries, clique c = {c, c + 16, ..., c + 240}: with rows = codes every clique sits in one bank
+    // group (entry % 16). Each clique's entries co-occur; a clique's members must end in 16 distinct groups.
+    for (int lanes : {16, 32}) {
+        std::vector<uint32_t> w(256 * 256, 0);
+        for (int a = 0; a < 256; ++a)
+            for (int b = 0; b < 256; ++b)
+                if (a != b && a % 16 == b % 16) w[a * 256 + b] = 5;
+        std::vector<uint8_t> rows(256);
+        vk::order::fit_rows(w.data(), lanes, rows.data());
+        EXPECT(is_permutation_of_rows(rows, 1));
+        bool spread = true;
+        for (int c = 0; c < 16; ++c) {
+            std::vector<int> groups;
+            for (int j = 0; j < 16; ++j) groups.push_back(rows[c + 16 * j] % lanes);
+            std::sort(groups.begin(), groups.end());
+            spread = spread && std::unique(groups.begin(), groups.end()) == groups.end();
+        }
+        EXPECT(spread);
+    }
+    std::vector<uint32_t> none(256 * 256, 0);
+    std::vector<uint8_t> rows(256);
+    vk::order::fit_rows(none.data(), 16, rows.data());
+    bool identity = true;
+    for (int e = 0; e < 256; ++e) identity = identity && rows[e] == e;
+    EXPECT(identity);  // nothing co-occurs: rows stay the codes
+}
+
+CASE("slot order: on clustered codes the fitted rows lower the modelled bank load") {
+    // Codes whose vectors draw each sub-space's entry from one of a few per-cluster sets that share a bank group.
+    const size_t n = 64 * 256, m = 16;
+    std::mt19937_64 rng(17);
+    std::vector<uint8_t> codes(n * m);
+    for (size_t i = 0; i < n; ++i) {
+        const int cluster = static_cast<int>(rng() % 64);
+        for (size_t s = 0; s < m; ++s) {
+            const int base = (cluster * 7 + static_cast<int>(s) * 3) % 16;  // the cluster's bank group in sub-space s
+            codes[i * m + s] = static_cast<uint8_t>(s < 4 ? cluster * 4 + rng() % 4 : base + 16 * (rng() % 16));
+        }
+    }
+    const vk::order::SlotOrder o = vk::order::slot_order(codes.data(), n, m, n, 16, 2);
+    auto vec = [&](size_t slot) { return size_t{o.ids[vk::order::interleaved(slot)]}; };
+    const double plain = bank_load(codes, n, m, 16, {}, vec), fitted = bank_load(codes, n, m, 16, o.rows, vec);
+    std::printf("    clustered codes, slot order: bank load with rows = codes %.3f, fitted rows %.3f\n", plain, fitted);
+    EXPECT(fitted < plain * 0.8);
 }

@@ -144,9 +144,9 @@ def test_final_merge_bound_equal_to_the_kth_best(variant):
     # The k best vectors each head a different block's list, so the bound (the k-th smallest head) is the k-th best
     # itself and exactly k pairs survive the filter: the pair equal to the bound must be kept. The 16 planted
     # vectors have first code bytes 16 apart and distances 0.05^2 .. 0.8^2, far below the random vectors' (~60).
-    # With 64 and 100 blocks they fall in 16 different blocks of the sorted, tile-spread layout (checked on the CPU
-    # against slot_order.hpp for this data); the default spread (37 blocks) puts two in one block and is kept as an
-    # ordinary parity case.
+    # With 64 and 100 blocks they fall in 16 different blocks of the layout the first search builds for its one-query
+    # (4-byte) table reads (checked on the CPU against slot_order.hpp for this data); the default block count is kept
+    # as an ordinary parity case.
     rng = np.random.default_rng(17)
     n, d, m = 300_007, 32, 16
     centroids = rng.standard_normal((m, 256, d // m)).astype(np.float32)

@@ -106,7 +106,7 @@ _SIGNATURES = {
     "vk_searcher_set_tuning": (ctypes.c_int, [_P, ctypes.POINTER(_Tuning)]),
     "vk_searcher_get_tuning": (ctypes.c_int, [_P, ctypes.POINTER(_Tuning)]),
     "vk_searcher_last_launch": (ctypes.c_int, [_P, ctypes.POINTER(_LaunchShape)]),
-    "vk_searcher_slot_ids": (ctypes.c_int, [_P, _P, ctypes.c_size_t]),
+    "vk_searcher_layout": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
     "vk_search": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _P,
                                  ctypes.POINTER(_Timings)]),
     "vk_distances": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P, ctypes.POINTER(_Timings)]),
@@ -312,12 +312,16 @@ class PQSearcher:
         _check(library().vk_searcher_get_tuning(self._h, ctypes.byref(c)))
         return Tuning(c.scan_threads, c.blocks_per_query, c.queries_per_block, c.vectors_per_step)
 
-    def slot_ids(self) -> np.ndarray:
-        """The v8/v9 layout's slot order: per slot of n padded to 256, the id of the vector scanned there,
-        interleaved by four tiles (vk_searcher_slot_ids)."""
-        out = np.empty((self.n + 255) // 256 * 256, dtype=np.uint32)
-        _check(library().vk_searcher_slot_ids(self._h, out.ctypes.data, out.size))
-        return out
+    def layout(self):
+        """The v8/v9 code layout (vk_searcher_layout): (ids, rows, lanes). ids: per slot of n padded to 256, the id
+        of the vector scanned there, interleaved by four tiles; rows: [m][256] LDS table row of each code value;
+        lanes: lanes per table-read pass the layout was built for."""
+        ids = np.empty((self.n + 255) // 256 * 256, dtype=np.uint32)
+        rows = np.empty((self.m, 256), dtype=np.uint8)
+        lanes = ctypes.c_int(0)
+        _check(library().vk_searcher_layout(self._h, ids.ctypes.data, ids.size, rows.ctypes.data, rows.size,
+                                            ctypes.byref(lanes)))
+        return ids, rows, lanes.value
 
     def last_launch(self) -> LaunchShape:
         s = _LaunchShape()

@@ -257,6 +257,8 @@ struct vk_searcher {
     DeviceBuffer<uint8_t> codes, codes_il;
     DeviceBuffer<uint4> codes_v, codes_s;  // words in vector order (v6, v7) and in sorted slot order (v8, v9)
     DeviceBuffer<uint32_t> slot_ids;        // the sorted slot order: the vector id of each slot (m % 16 == 0 only)
+    DeviceBuffer<uint8_t> table_rows;       // [m][256]: the LDS table row of each code value in the sorted layout
+    int order_lanes = 0;                    // lanes per table-read pass the slot order was built for
     DeviceBuffer<Pair> part, out;
     PinnedBuffer<float> staged_q;     // host-buffer searches: queries and results staged in page-locked memory
     PinnedBuffer<Pair> staged_out;
@@ -279,7 +281,9 @@ struct vk_searcher {
             require(m * vk::KSUB * sizeof(float) <= info.max_smem_per_block, "LUT does not fit in LDS");
     }
 
-    void ensure_layout(int v) {
+    // lanes: lanes per pass of the table reads the v8/v9 searches make (search_lanes); the sorted layout is built
+    // once, for the first search that needs it.
+    void ensure_layout(int v, int lanes = 16) {
         bool built = false;
         if (vk::plan::uses_byte_layout(v) && !have_il) {
             codes_il.ensure(static_cast<size_t>(n_pad) * m);
@@ -292,37 +296,71 @@ struct vk_searcher {
             have_v = built = true;
         }
         if (vk::plan::uses_sorted_layout(v) && !have_s) {
-            ensure_slot_ids();
+            ensure_slot_ids(lanes);
             codes_s.ensure(static_cast<size_t>(n_pad) * (m / 16));
             VK_HIP(vk::launch_build_sorted_words(codes.get(), n, static_cast<int>(m), n_pad, slot_ids.get(),
-                                                 codes_s.get(), stream));
+                                                 table_rows.get(), codes_s.get(), stream));
             have_s = built = true;
         }
         if (built) VK_HIP(hipStreamSynchronize(stream));  // a layout kernel's failure surfaces here, not mid-search
     }
 
-    // The slot order of the fused scans' layout (slot_order.hip, the order of slot_order.hpp), built on the GPU the
-    // first time a v8/v9 search (or vk_searcher_slot_ids) needs it; its scratch is freed right after.
-    void ensure_slot_ids() {
+    // The slot order and table rows of the fused scans' layout (slot_order.hpp), for table reads of `lanes` lanes
+    // per pass, built the first time a v8/v9 search (or vk_searcher_slot_ids) needs them: on the GPU
+    // (slot_order.hip: sort, co-occurrence counts, dealing) with the rows fitted on the host between its two
+    // launches, or for m > 64 wholly on the host; the scratch is freed right after.
+    void ensure_slot_ids(int lanes) {
         if (have_slot_ids) return;
         require(m % 16 == 0, "the sorted code layout needs m % 16 == 0");
         slot_ids.ensure(static_cast<size_t>(n_pad));
-        if (m > 64) {  // beyond the GPU kernel's LDS sizing: the same order computed on the host
+        table_rows.ensure(m * vk::KSUB);
+        const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+        if (m > 64) {  // beyond the GPU kernels' LDS sizing
             std::vector<uint8_t> host_codes(n * m);
             VK_HIP(hipMemcpy(host_codes.data(), codes.get(), n * m, hipMemcpyDeviceToHost));
-            const std::vector<uint32_t> order = vk::order::slot_ids(host_codes.data(), n, m, static_cast<size_t>(n_pad));
-            VK_HIP(hipMemcpy(slot_ids.get(), order.data(), order.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
-            have_slot_ids = true;
-            return;
+            const vk::order::SlotOrder order =
+                vk::order::slot_order(host_codes.data(), n, m, static_cast<size_t>(n_pad), lanes, threads);
+            VK_HIP(hipMemcpy(slot_ids.get(), order.ids.data(), order.ids.size() * sizeof(uint32_t),
+                             hipMemcpyHostToDevice));
+            VK_HIP(hipMemcpy(table_rows.get(), order.rows.data(), order.rows.size(), hipMemcpyHostToDevice));
+        } else {
+            size_t bytes = 0;
+            VK_HIP(vk::slot_order_scratch_bytes(static_cast<int64_t>(n), static_cast<int>(m), &bytes));
+            DeviceBuffer<unsigned char> scratch;
+            scratch.ensure(bytes);
+            const uint32_t* d_counts = nullptr;
+            VK_HIP(vk::launch_slot_sort(codes.get(), static_cast<int64_t>(n), static_cast<int>(m), lanes,
+                                        scratch.get(), bytes, &d_counts, stream));
+            std::vector<uint32_t> counts(m * vk::KSUB * vk::KSUB);
+            VK_HIP(hipMemcpyAsync(counts.data(), d_counts, counts.size() * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                  stream));
+            VK_HIP(hipStreamSynchronize(stream));
+            vk::order::mirror_counts(counts, m);
+            const std::vector<uint8_t> rows = vk::order::fit_all_rows(counts, m, lanes, threads);
+            VK_HIP(hipMemcpyAsync(table_rows.get(), rows.data(), rows.size(), hipMemcpyHostToDevice, stream));
+            VK_HIP(vk::launch_slot_place(codes.get(), static_cast<int64_t>(n), static_cast<int>(m), n_pad, lanes,
+                                         scratch.get(), bytes, table_rows.get(), slot_ids.get(), stream));
+            VK_HIP(hipStreamSynchronize(stream));
         }
-        size_t bytes = 0;
-        VK_HIP(vk::slot_order_scratch_bytes(static_cast<int64_t>(n), &bytes));
-        DeviceBuffer<unsigned char> scratch;
-        scratch.ensure(bytes);
-        VK_HIP(vk::launch_slot_order(codes.get(), static_cast<int64_t>(n), static_cast<int>(m), n_pad, scratch.get(),
-                                     bytes, slot_ids.get(), stream));
-        VK_HIP(hipStreamSynchronize(stream));
+        order_lanes = lanes;
         have_slot_ids = true;
+    }
+
+    // Queries per block of a v8/v9 batch of b queries with k results.
+    int wave_q(size_t b, size_t kk, bool f16) const {
+        const size_t entry_bytes = f16 ? 2 : sizeof(float);
+        return vk::plan::cap_q_by_batch(vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block,
+                                                              false, static_cast<int>(kk), entry_bytes),
+                                        b);
+    }
+
+    // Lanes per pass of the table reads of a search of nq queries: fp32 tables read 4 * min(Q, 4) bytes per entry
+    // (8 queries are two 4-query tables), fp16 tables 2 * Q.
+    int search_lanes(int v, size_t nq, size_t kk) const {
+        if (!vk::plan::uses_sorted_layout(v)) return 16;
+        const bool f16 = v == VK_V9_FUSED_WARP_F16;
+        const int q = wave_q(std::min(query_batch(v), nq), kk, f16);
+        return vk::order::pass_lanes(f16 ? 2 * q : 4 * std::min(q, 4));
     }
 
     // The stage clock of this searcher's calls: its events are created once and reused by every call.
@@ -350,8 +388,7 @@ struct vk_searcher {
         w.K = static_cast<int>(kk);
         const int segments = w.K <= vk::WAVE ? 1 : 2;
         const size_t entry_bytes = f16 ? 2 : sizeof(float);
-        w.q = vk::plan::cap_q_by_batch(
-            vk::plan::effective_q(tuning.queries_per_block, m, info.max_smem_per_block, false, w.K, entry_bytes), b);
+        w.q = wave_q(b, kk, f16);
         // fp32: 8 queries are two groups of 4 (16-byte reads); fp16: up to 8 queries in one group.
         const int qg = (!f16 && w.q == 8) ? 4 : w.q, ng = (!f16 && w.q == 8) ? 2 : 1;
         w.ilp = tuning.vectors_per_step;
@@ -431,6 +468,7 @@ struct vk_searcher {
         a.centroids = centroids.get();
         a.codes = codes_s.get();
         a.slot_ids = slot_ids.get();
+        a.table_rows = table_rows.get();
         a.n = static_cast<int64_t>(n);
         a.d = static_cast<int>(d);
         a.m = static_cast<int>(m);
@@ -605,7 +643,7 @@ struct vk_searcher {
     void search_host(const float* host_q, size_t nq, size_t kk, int v, vk_neighbor* host_out, vk_timings* t) {
         check_search(kk, v);
         use_device();
-        ensure_layout(v);
+        ensure_layout(v, search_lanes(v, nq, kk));
         StageClock& clock = stage_clock();
         const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
@@ -633,7 +671,7 @@ struct vk_searcher {
     void search_device(const float* d_q, size_t nq, size_t kk, int v, vk_neighbor* d_out, vk_timings* t) {
         check_search(kk, v);
         use_device();
-        ensure_layout(v);
+        ensure_layout(v, search_lanes(v, nq, kk));
         StageClock& clock = stage_clock();
         const size_t batch = query_batch(v);
         for (size_t q0 = 0; q0 < nq; q0 += batch) {
@@ -882,15 +920,20 @@ VK_EXPORT int vk_searcher_last_launch(const vk_searcher* s, vk_launch_shape* out
     });
 }
 
-VK_EXPORT int vk_searcher_slot_ids(vk_searcher* s, uint32_t* out, size_t count) {
+VK_EXPORT int vk_searcher_layout(vk_searcher* s, uint32_t* ids, size_t ids_count, uint8_t* rows,
+                                 size_t rows_count, int* lanes) {
     return guarded([&] {
-        require(s != nullptr && out != nullptr, "null argument");
-        if (count != static_cast<size_t>(s->n_pad))
-            fail(VK_ERR_INVALID_ARGUMENT, "count must be n rounded up to a multiple of 256");
+        require(s != nullptr && ids != nullptr, "null argument");
+        if (ids_count != static_cast<size_t>(s->n_pad))
+            fail(VK_ERR_INVALID_ARGUMENT, "ids_count must be n rounded up to a multiple of 256");
+        if (rows == nullptr ? rows_count != 0 : rows_count != s->m * vk::KSUB)
+            fail(VK_ERR_INVALID_ARGUMENT, "rows_count must be m * 256 (or 0 with rows NULL)");
         if (s->m % 16 != 0) fail(VK_ERR_INVALID_ARGUMENT, "the sorted layout needs m % 16 == 0");
         s->use_device();
-        s->ensure_slot_ids();
-        VK_HIP(hipMemcpy(out, s->slot_ids.get(), count * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        s->ensure_slot_ids(s->order_lanes ? s->order_lanes : 16);
+        VK_HIP(hipMemcpy(ids, s->slot_ids.get(), ids_count * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        if (rows) VK_HIP(hipMemcpy(rows, s->table_rows.get(), rows_count, hipMemcpyDeviceToHost));
+        if (lanes) *lanes = s->order_lanes;
     });
 }
 

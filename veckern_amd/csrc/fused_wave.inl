@@ -297,9 +297,10 @@ __device__ __forceinline__ void table_entries(const WaveScanArgs& a, const float
     else table_entries_w<QS, M, W, 0>(a, qrow, wave, lane, sink);
 }
 
-// Writes the NG query-interleaved tables of a slab into LDS, interleaved per sub-space: group t's entries of
-// sub-space s are the 256 entries at ((s * NG + t) * 256 + c) * entry bytes, so the NG reads of one code byte lie
-// within 256 * NG entries of each other and share one address register (immediate offsets). fp16 tables take each
+// Writes the NG query-interleaved tables of a slab into LDS, interleaved per sub-space: group t's entry for code c
+// of sub-space s is at ((s * NG + t) * 256 + row) * entry bytes, row = a.table_rows[s * 256 + c] (the row the code
+// layout stores for c) or c, so the NG reads of one code byte lie within 256 * NG entries of each other and share
+// one address register (immediate offsets). fp16 tables take each
 // query's power-of-two shift from the per-query maxima in `qmax` (raw fp32 bits).
 template <int QG, int NG, int M, int W, bool F16>
 __device__ __forceinline__ void build_tables(const WaveScanArgs& a, const float* const (&qrow)[QG * NG],
@@ -314,7 +315,8 @@ __device__ __forceinline__ void build_tables(const WaveScanArgs& a, const float*
 #pragma unroll
             for (int q = 0; q < QG; ++q) group[q] = qrow[t * QG + q];
             auto sink = [&](int s, int c, const float* acc) {
-                unsigned char* dst = tables + ((s * NG + t) * KSUB + c) * EB;
+                const int row = a.table_rows ? a.table_rows[s * KSUB + c] : c;
+                unsigned char* dst = tables + ((s * NG + t) * KSUB + row) * EB;
                 if constexpr (QG == 4) *reinterpret_cast<float4*>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
                 else if constexpr (QG == 2) *reinterpret_cast<float2*>(dst) = make_float2(acc[0], acc[1]);
                 else *reinterpret_cast<float*>(dst) = acc[0];
@@ -329,9 +331,10 @@ __device__ __forceinline__ void build_tables(const WaveScanArgs& a, const float*
             uint32_t h[QS];
 #pragma unroll
             for (int q = 0; q < QS; ++q) h[q] = to_half_bits(ldexpf(acc[q], -shift[q]));
+            const int row = a.table_rows ? a.table_rows[s * KSUB + c] : c;
 #pragma unroll
             for (int t = 0; t < NG; ++t) {
-                unsigned char* dst = tables + ((s * NG + t) * KSUB + c) * EB;
+                unsigned char* dst = tables + ((s * NG + t) * KSUB + row) * EB;
                 const uint32_t* g = h + t * QG;
                 if constexpr (QG == 8)
                     *reinterpret_cast<uint4*>(dst) = make_uint4(g[0] | g[1] << 16, g[2] | g[3] << 16,

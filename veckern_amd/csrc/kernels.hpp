@@ -19,19 +19,26 @@ hipError_t launch_lut(const float* queries, const float* centroids, int d, int m
 // Word-interleaved: out[(tile * (m/16) + w) * 64 + lane] = 16 sub-codes 16w..16w+15 of vector tile*64+lane.
 hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint4* out, hipStream_t stream);
 // The word-interleaved layout in the fused scans' slot order: slot j holds vector slot_ids[j's interleaved
-// position]; slots [n, n_pad) are zero.
+// position], each code byte c of sub-space s replaced by rows[s * 256 + c] (rows == nullptr: c itself); slots
+// [n, n_pad) are zero.
 hipError_t launch_build_sorted_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, const uint32_t* slot_ids,
-                                     uint4* out, hipStream_t stream);
+                                     const uint8_t* rows, uint4* out, hipStream_t stream);
 // Byte-interleaved: out[(tile * m + s) * 64 + lane] = sub-code s of vector tile*64+lane.
 hipError_t launch_build_bytes(const uint8_t* codes, int64_t n, int m, int64_t n_pad, uint8_t* out,
                               hipStream_t stream);
 // Zeroes count 32-bit words with a kernel (no memset node).
 hipError_t launch_zero_words(unsigned* p, int64_t count, hipStream_t stream);
-// The fused scans' slot order on the GPU (slot_order.hip), equal to order::slot_ids of slot_order.hpp: `out` receives
-// n_pad interleaved slot ids (padding slots 0). scratch: slot_order_scratch_bytes(n) bytes of device memory.
-hipError_t slot_order_scratch_bytes(int64_t n, size_t* bytes);
-hipError_t launch_slot_order(const uint8_t* codes, int64_t n, int m, int64_t n_pad, void* scratch,
-                             size_t scratch_bytes, uint32_t* out, hipStream_t stream);
+// The fused scans' slot order and table rows on the GPU (slot_order.hip), equal to order::slot_order of
+// slot_order.hpp for m <= 64 and lanes 16, 32 or 64, in two launches around the host's fit of the rows:
+// launch_slot_sort sorts the vectors and leaves, in scratch, the co-occurrence counts of the sampled blocks' passes
+// (`*counts`: [m][256][256] words, entries [s][a][b] with a < b filled, the rest zero); the host fits the rows
+// (order::fit_rows on the mirrored counts) and launch_slot_place, with the same scratch, deals the blocks and writes
+// the n_pad interleaved slot ids to `out` (padding slots 0). scratch: slot_order_scratch_bytes(n, m) bytes.
+hipError_t slot_order_scratch_bytes(int64_t n, int m, size_t* bytes);
+hipError_t launch_slot_sort(const uint8_t* codes, int64_t n, int m, int lanes, void* scratch, size_t scratch_bytes,
+                            const uint32_t** counts, hipStream_t stream);
+hipError_t launch_slot_place(const uint8_t* codes, int64_t n, int m, int64_t n_pad, int lanes, void* scratch,
+                             size_t scratch_bytes, const uint8_t* rows, uint32_t* out, hipStream_t stream);
 
 // ---- fused scan with wave-cooperative lists (fused_wave_*.hip)
 struct WaveScanArgs {
@@ -41,6 +48,8 @@ struct WaveScanArgs {
                              // layout, slot order given by slot_ids)
     const uint32_t* slot_ids;  // exhaustive scans: per slot, its vector's id, interleaved by four tiles
                                // ([tile / 4][lane][tile % 4])
+    const uint8_t* table_rows;  // exhaustive scans: [m][256] LDS table row of each code value (the layout stores
+                                // rows, not codes); nullptr: row = code
     int64_t n;
     int d;
     int m;

@@ -42,7 +42,8 @@ hipError_t launch_build_words(const uint8_t* codes, int64_t n, int m, int64_t n_
 
 __global__ void __launch_bounds__(256)
     build_sorted_words_kernel(const uint8_t* __restrict__ codes, int64_t n, int words, int64_t total,
-                              const uint32_t* __restrict__ slot_ids, uint4* __restrict__ out) {
+                              const uint32_t* __restrict__ slot_ids, const uint8_t* __restrict__ rows,
+                              uint4* __restrict__ out) {
     for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total;
          o += static_cast<int64_t>(gridDim.x) * 256) {
         const int64_t lane = o % WAVE, w = (o / WAVE) % words, tile = o / (static_cast<int64_t>(WAVE) * words);
@@ -51,17 +52,30 @@ __global__ void __launch_bounds__(256)
         if (slot < n) {
             const int64_t i = slot_ids[(tile >> 2) * 256 + lane * 4 + (tile & 3)];
             if (i < n) v = *reinterpret_cast<const uint4*>(codes + (i * words + w) * 16);  // ids are < n
+            if (rows) {  // code byte j of the word (sub-space 16 w + j) -> its table row
+                const uint8_t* r = rows + w * 16 * 256;
+                uint32_t x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t y = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        y |= static_cast<uint32_t>(r[(k * 4 + b) * 256 + ((x[k] >> (8 * b)) & 0xffu)]) << (8 * b);
+                    x[k] = y;
+                }
+                v = make_uint4(x[0], x[1], x[2], x[3]);
+            }
         }
         out[o] = v;
     }
 }
 
 hipError_t launch_build_sorted_words(const uint8_t* codes, int64_t n, int m, int64_t n_pad, const uint32_t* slot_ids,
-                                     uint4* out, hipStream_t stream) {
+                                     const uint8_t* rows, uint4* out, hipStream_t stream) {
     const int words = m / 16;
     const int64_t total = n_pad * words;
     hipLaunchKernelGGL(build_sorted_words_kernel, dim3(layout_grid(total)), dim3(256), 0, stream, codes, n, words, total,
-                       slot_ids, out);
+                       slot_ids, rows, out);
     return hipGetLastError();
 }
 

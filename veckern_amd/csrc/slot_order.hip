@@ -1,8 +1,10 @@
-// The fused scans' slot order built on the GPU: the same order as slot_order.hpp (vectors sorted by their first
-// four code bytes, little-sharing 256-slot blocks dealt over their 16 passes by bank group, the blocks' 64-slot tiles
-// spread over the layout, ids interleaved by four tiles), slot for slot. The sort is a stable radix sort of
-// (key, id) pairs; each 256-slot block is then ordered by one wave, with the block's code rows, entry-present masks
-// and bank-group counts in LDS.
+// The fused scans' code layout built on the GPU: the same slot order and table rows as slot_order.hpp (vectors
+// sorted by their first four code bytes, table rows fitted to the sorted passes' co-occurrences, full 256-slot
+// blocks dealt over their passes by bank group where that pays, tiles spread, ids interleaved), slot for slot.
+// The sort is a stable radix sort of (key, id) pairs; the co-occurrence counts of the sampled blocks are
+// accumulated with atomics; the fit of the rows (a few milliseconds per sub-space) runs on the host between the two
+// launches; each block is then ordered by one wave, with its code rows, entry-present masks and bank-group counts
+// in LDS.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
@@ -12,9 +14,8 @@
 namespace vk {
 namespace {
 
-constexpr int kBlockSlots = static_cast<int>(order::kBlock);  // 256 slots: 16 passes of 16 lanes
-constexpr int kPasses = order::kPasses;
-constexpr int kLanes = order::kLanes;
+constexpr int kBlockSlots = static_cast<int>(order::kBlock);  // 256 slots: one wave step of four tiles
+constexpr int kRows = order::kEntries;                         // 256 table rows per sub-space
 
 // keys[i]: row i's first four code bytes, big-endian (missing bytes 0); ids[i] = i.
 __global__ void __launch_bounds__(256) slot_keys_kernel(const uint8_t* __restrict__ codes, int64_t n, int m,
@@ -29,61 +30,60 @@ __global__ void __launch_bounds__(256) slot_keys_kernel(const uint8_t* __restric
     }
 }
 
-// Wave-wide sum of one value per lane.
-__device__ __forceinline__ unsigned wave_sum(unsigned v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) v += static_cast<unsigned>(__shfl_xor(static_cast<int>(v), o));
-    return v;
-}
-
-// order::block_stats of the block whose rows (in LDS, [256][m]) are read in `slot_order` (local row per slot): lane l
-// takes the (pass, sub-space) pairs l, l + 64, ...; returns {load, distinct} summed over the wave. Per pair, the 16
-// entries are compared pairwise in registers: an entry is new when no earlier lane read it, and the largest number
-// of new entries in one bank group (entry mod 16) is the running count order::block_stats takes the maximum of.
-template <int M>
-__device__ order::BlockStats block_stats(const uint8_t* rows, int m, const uint8_t* slot_order, int lane) {
-    const int mm = M ? M : m;
-    unsigned load = 0, distinct = 0;
-    for (int pair = lane; pair < kPasses * mm; pair += WAVE) {
-        const int p = pair / mm, s = pair % mm;
-        unsigned e[kLanes];
-#pragma unroll
-        for (int l = 0; l < kLanes; ++l) e[l] = rows[slot_order[p * kLanes + l] * mm + s];
-        unsigned fresh = 0, mx = 0;  // fresh: bit l set when lane l's entry is new
-#pragma unroll
-        for (int l = 0; l < kLanes; ++l) {
-            bool seen = false;
-            unsigned same_group = 1;
-#pragma unroll
-            for (int k = 0; k < l; ++k) {
-                seen = seen || e[k] == e[l];
-                same_group += ((fresh >> k) & 1u) && ((e[k] ^ e[l]) & 15u) == 0 ? 1u : 0u;
-            }
-            if (!seen) {
-                fresh |= 1u << l;
-                ++distinct;
-                mx = same_group > mx ? same_group : mx;
-            }
+// Co-occurrence counts of the sampled blocks (order::cooccurrence), upper triangle only: w[(s * 256 + a) * 256 + b]
+// for a < b. One workgroup per sampled block; thread t takes the (pass, sub-space) pairs t, t + 256, ...: it gathers
+// the pass's entries, keeps the distinct ones in its LDS row and adds one to every pair of them.
+template <int L>
+__global__ void __launch_bounds__(256) cooccurrence_kernel(const uint8_t* __restrict__ codes, int m,
+                                                             const uint32_t* __restrict__ sorted, int64_t full,
+                                                             int64_t samples, uint32_t* __restrict__ w) {
+    __shared__ uint8_t seen[256][L];
+    const int64_t i = blockIdx.x;
+    if (i >= samples) return;
+    const uint32_t* block = sorted + (i * full / samples) * kBlockSlots;
+    uint8_t* list = seen[threadIdx.x];
+    constexpr int P = kBlockSlots / L;
+    for (int c = threadIdx.x; c < P * m; c += 256) {
+        const int p = c / m, s = c % m;
+        int k = 0;
+        for (int l = 0; l < L; ++l) {
+            const uint8_t e = codes[static_cast<int64_t>(block[p * L + l]) * m + s];
+            bool found = false;
+            for (int j = 0; j < k; ++j) found = found || list[j] == e;
+            if (!found) list[k++] = e;
         }
-        load += mx;
+        uint32_t* ws = w + static_cast<int64_t>(s) * kRows * kRows;
+        for (int a = 0; a < k; ++a)
+            for (int b = a + 1; b < k; ++b) {
+                const unsigned x = list[a], y = list[b];
+                atomicAdd(ws + (x < y ? x * kRows + y : y * kRows + x), 1u);
+            }
     }
-    return {wave_sum(load), wave_sum(distinct)};
 }
 
-// One full 256-slot block per wave: the block's rows are gathered into LDS; if its sorted passes read at least
-// kDealMinDistinct distinct entries per (pass, sub-space) on average, its vectors are dealt over the 16 passes
-// first-fit (order::deal_block, one vector at a time: lane (p, s-group) sums pass p's cost over its sub-spaces, the
-// wave picks the cheapest pass with room, lowest first on ties) and the dealt order is kept if its load is lower.
+// One 256-slot block per wave (order::order_blocks): the block's code rows are gathered into LDS. Its sorted
+// passes' statistics (order::block_stats: the sum over (pass, sub-space) of the largest bank-group count of distinct
+// entries, and the number of distinct entries) are taken by filling the passes in slot order with the same
+// bookkeeping the dealing keeps: `present[s * 256 + e]` (bit p: pass p reads entry e of sub-space s),
+// `count[(s * L + g) * P + p]` (pass p's distinct entries in group g of sub-space s) and `top[s * P + p]` (the
+// largest such count), lane s updating sub-space s. If the block reads at least kDealMinDistinct * m distinct
+// entries, its vectors are dealt (order::deal_block: lane (p, s-group) sums pass p's cost over its sub-spaces, the
+// wave picks the cheapest pass with room, lowest first on ties), and the dealt order is kept if its load is lower.
 // The block's ids are then written at their spread, interleaved slots. Partial last block: ids in sorted order.
-template <int M>
+template <int M, int L>
 __global__ void __launch_bounds__(64) order_blocks_kernel(const uint8_t* __restrict__ codes, int64_t n, int m,
-                                                            const uint32_t* __restrict__ sorted, int64_t blocks,
+                                                            const uint32_t* __restrict__ sorted,
+                                                            const uint8_t* __restrict__ table_rows, int64_t blocks,
                                                             int64_t tiles, int64_t stride, uint32_t* __restrict__ out) {
     constexpr int MM = M ? M : 64;  // LDS sized for the largest m when m is not fixed (m <= 64)
+    constexpr int P = kBlockSlots / L;
+    constexpr unsigned kRaise = L > 16 ? 2u : 0u;  // order::raise_penalty(L)
     __shared__ uint8_t rows[kBlockSlots * MM];
-    __shared__ uint16_t present[MM * 256];
-    __shared__ uint8_t groups[MM * 16 * kPasses];
-    __shared__ uint8_t local[kBlockSlots], dealt[kBlockSlots];
+    __shared__ uint8_t group[MM * kRows];
+    __shared__ uint16_t present[MM * kRows];
+    __shared__ uint8_t count[MM * L * P];
+    __shared__ uint8_t top[MM * P];
+    __shared__ uint8_t dealt[kBlockSlots];
     const int lane = threadIdx.x;
     const int mm = M ? M : m;
     const int64_t blk = blockIdx.x;
@@ -95,70 +95,102 @@ __global__ void __launch_bounds__(64) order_blocks_kernel(const uint8_t* __restr
         const int64_t slot = t < tiles * 64 ? (t / 64) * stride % tiles * 64 + t % 64 : t;
         return (slot / 64 / 4) * 256 + (slot % 64) * 4 + (slot / 64) % 4;
     };
-    // Slots in sorted order (every block, the partial last one included), unless the block's dealt order is kept.
-    for (int i = lane; i < kBlockSlots; i += WAVE) local[i] = static_cast<uint8_t>(i);
-    const uint8_t* order_used = local;
+    bool use_dealt = false;
     if (cnt == kBlockSlots) {
         for (int e = lane; e < kBlockSlots * mm; e += WAVE) rows[e] = codes[static_cast<int64_t>(block[e / mm]) * mm + e % mm];
-    }
-    __syncthreads();
-    if (cnt == kBlockSlots) {
-        const order::BlockStats st = block_stats<M>(rows, mm, local, lane);
-        if (st.distinct >= order::kDealMinDistinct * kPasses * mm) {
-            for (int e = lane; e < mm * 256; e += WAVE) present[e] = 0;
-            for (int e = lane; e < mm * 16 * kPasses; e += WAVE) groups[e] = 0;
+        for (int e = lane; e < mm * kRows; e += WAVE) group[e] = static_cast<uint8_t>(table_rows[e] % L);
+        auto reset = [&] {
+            for (int e = lane; e < mm * kRows; e += WAVE) present[e] = 0;
+            for (int e = lane; e < mm * L * P; e += WAVE) count[e] = 0;
+            for (int e = lane; e < mm * P; e += WAVE) top[e] = 0;
+        };
+        // Adds row i to pass p in sub-space s = lane (one sub-space per lane); returns whether its entry is new.
+        auto add = [&](int i, int p) {
+            if (lane >= mm) return 0u;
+            const int s = lane;
+            const unsigned e = rows[i * mm + s];
+            const uint16_t mask = present[s * kRows + e];
+            if ((mask >> p) & 1u) return 0u;
+            present[s * kRows + e] = static_cast<uint16_t>(mask | (1u << p));
+            const int c = ++count[(s * L + group[s * kRows + e]) * P + p];
+            if (c > top[s * P + p]) top[s * P + p] = static_cast<uint8_t>(c);
+            return 1u;
+        };
+        auto load = [&] {  // sum of top over (sub-space, pass)
+            unsigned t = 0;
+            for (int e = lane; e < mm * P; e += WAVE) t += top[e];
+            for (int o = WAVE / 2; o > 0; o >>= 1) t += static_cast<unsigned>(__shfl_xor(static_cast<int>(t), o));
+            return t;
+        };
+        reset();
+        __syncthreads();
+        unsigned distinct = 0;
+        for (int i = 0; i < kBlockSlots; ++i) distinct += add(i, i / L);  // lane s touches sub-space s only
+        __syncthreads();
+        for (int o = WAVE / 2; o > 0; o >>= 1) distinct += static_cast<unsigned>(__shfl_xor(static_cast<int>(distinct), o));
+        const unsigned sorted_load = load();
+        if (distinct >= order::kDealMinDistinct * static_cast<unsigned>(mm)) {
             __syncthreads();
-            const int p = lane % kPasses, s0 = lane / kPasses;  // this lane's pass and first sub-space (of 4)
-            int fill = 0;                                      // lanes p: vectors dealt to pass p so far
+            reset();
+            __syncthreads();
+            const int p = lane % P, s0 = lane / P;  // this lane's pass and first sub-space
+            int fill = 0;                          // lanes of pass p: vectors dealt to pass p so far
             for (int i = 0; i < kBlockSlots; ++i) {
                 const uint8_t* row = rows + i * mm;
                 unsigned cost = 0;
-                for (int s = s0; s < mm; s += WAVE / kPasses) {
+                for (int s = s0; s < mm; s += WAVE / P) {
                     const unsigned e = row[s];
-                    cost += ((present[s * 256 + e] >> p) & 1u) ? 0u : groups[(s * 16 + (e & 15)) * kPasses + p];
+                    if ((present[s * kRows + e] >> p) & 1u) continue;
+                    const unsigned c = count[(s * L + group[s * kRows + e]) * P + p];
+                    const unsigned t = top[s * P + p];
+                    cost += c + (c + 1u > (t > 1u ? t : 1u) ? kRaise : 0u);
                 }
-                cost += static_cast<unsigned>(__shfl_xor(static_cast<int>(cost), 16));
-                cost += static_cast<unsigned>(__shfl_xor(static_cast<int>(cost), 32));
-                // Cheapest pass with room, lowest pass on ties: the minimum of (cost, pass) over passes with room.
-                unsigned key = fill < kLanes ? (cost << 4) | static_cast<unsigned>(p) : 0xffffffffu;
 #pragma unroll
-                for (int o = 1; o < kPasses; o <<= 1) {
+                for (int o = P; o < WAVE; o <<= 1) cost += static_cast<unsigned>(__shfl_xor(static_cast<int>(cost), o));
+                // Cheapest pass with room, lowest pass on ties: the minimum of (cost, pass) over passes with room.
+                unsigned key = fill < L ? (cost << 4) | static_cast<unsigned>(p) : 0xffffffffu;
+#pragma unroll
+                for (int o = 1; o < P; o <<= 1) {
                     const unsigned other = static_cast<unsigned>(__shfl_xor(static_cast<int>(key), o));
                     key = other < key ? other : key;
                 }
                 const int best = static_cast<int>(key & 15u);
-                const int at = __shfl(fill, best);  // the best pass's fill before this vector
-                __syncthreads();  // every lane has read present / groups for this vector
-                for (int s = lane; s < mm; s += WAVE) {
-                    const unsigned e = row[s];
-                    const uint16_t mask = present[s * 256 + e];
-                    if ((mask >> best) & 1u) continue;
-                    present[s * 256 + e] = static_cast<uint16_t>(mask | (1u << best));
-                    ++groups[(s * 16 + (e & 15)) * kPasses + best];
-                }
-                if (lane == 0) dealt[best * kLanes + at] = static_cast<uint8_t>(i);
+                const int at = __shfl(fill, best);  // the best pass's fill before this vector (lane best: pass best)
+                __syncthreads();                    // every lane has read present / count / top for this vector
+                add(i, best);
+                if (lane == 0) dealt[best * L + at] = static_cast<uint8_t>(i);
                 if (p == best) ++fill;
                 __syncthreads();
             }
-            if (block_stats<M>(rows, mm, dealt, lane).load < st.load) order_used = dealt;
+            use_dealt = load() < sorted_load;
         }
     }
-    for (int j = lane; j < cnt; j += WAVE) out[place(b0 + j)] = block[order_used[j]];
+    __syncthreads();
+    for (int j = lane; j < cnt; j += WAVE) out[place(b0 + j)] = block[use_dealt ? dealt[j] : j];
 }
 
-template <int M>
-hipError_t launch_order_blocks(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, int64_t blocks,
-                               int64_t tiles, int64_t stride, uint32_t* out, hipStream_t stream) {
-    hipLaunchKernelGGL(order_blocks_kernel<M>, dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream, codes, n, m,
-                       sorted, blocks, tiles, stride, out);
+template <int M, int L>
+hipError_t launch_order_blocks(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, const uint8_t* rows,
+                               int64_t blocks, int64_t tiles, int64_t stride, uint32_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL((order_blocks_kernel<M, L>), dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream, codes,
+                       n, m, sorted, rows, blocks, tiles, stride, out);
     return hipGetLastError();
 }
 
-}  // namespace
+template <int L>
+hipError_t launch_order_blocks_m(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, const uint8_t* rows,
+                                 int64_t blocks, int64_t tiles, int64_t stride, uint32_t* out, hipStream_t stream) {
+    switch (m) {
+        case 16: return launch_order_blocks<16, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
+        case 32: return launch_order_blocks<32, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
+        case 64: return launch_order_blocks<64, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
+        default: return launch_order_blocks<0, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
+    }
+}
 
 // Scratch of the slot order: the radix sort's temporary storage first (at the allocation's aligned start), then keys,
-// ids, sorted keys and sorted ids (n words each).
-static size_t sort_temp_bytes(int64_t n, hipError_t* e) {
+// ids, sorted keys and sorted ids (n words each), then the co-occurrence counts (m * 256 * 256 words).
+size_t sort_temp_bytes(int64_t n, hipError_t* e) {
     size_t sort_bytes = 0;
     *e = hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
                                             static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
@@ -166,42 +198,87 @@ static size_t sort_temp_bytes(int64_t n, hipError_t* e) {
     return (sort_bytes + 255) / 256 * 256;
 }
 
-hipError_t slot_order_scratch_bytes(int64_t n, size_t* bytes) {
+struct ScratchParts {
+    void* temp;
+    size_t temp_bytes;
+    uint32_t *keys, *ids, *keys_sorted, *sorted, *counts;
+};
+
+hipError_t scratch_parts(void* scratch, size_t scratch_bytes, int64_t n, int m, ScratchParts* sp) {
     hipError_t e;
-    *bytes = sort_temp_bytes(n, &e) + 4 * static_cast<size_t>(n) * sizeof(uint32_t);
+    sp->temp_bytes = sort_temp_bytes(n, &e);
+    if (e != hipSuccess) return e;
+    const size_t words = (4 * static_cast<size_t>(n) + 63) / 64 * 64;
+    if (scratch_bytes < sp->temp_bytes + (words + static_cast<size_t>(m) * kRows * kRows) * sizeof(uint32_t))
+        return hipErrorInvalidValue;
+    sp->temp = scratch;
+    sp->keys = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(scratch) + sp->temp_bytes);
+    sp->ids = sp->keys + n;
+    sp->keys_sorted = sp->ids + n;
+    sp->sorted = sp->keys_sorted + n;
+    sp->counts = sp->keys + words;
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t slot_order_scratch_bytes(int64_t n, int m, size_t* bytes) {
+    hipError_t e;
+    const size_t words = (4 * static_cast<size_t>(n) + 63) / 64 * 64;
+    *bytes = sort_temp_bytes(n, &e) + (words + static_cast<size_t>(m) * kRows * kRows) * sizeof(uint32_t);
     return e;
 }
 
-hipError_t launch_slot_order(const uint8_t* codes, int64_t n, int m, int64_t n_pad, void* scratch,
-                             size_t scratch_bytes, uint32_t* out, hipStream_t stream) {
-    if (n <= 0 || m <= 0 || m > 64 || n > (int64_t{1} << 31) - 1) return hipErrorInvalidValue;
-    hipError_t e;
-    size_t temp_bytes = sort_temp_bytes(n, &e);
-    if (e != hipSuccess) return e;
-    if (scratch_bytes < temp_bytes + 4 * static_cast<size_t>(n) * sizeof(uint32_t)) return hipErrorInvalidValue;
-    void* temp = scratch;
-    uint32_t* keys = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(scratch) + temp_bytes);
-    uint32_t* ids = keys + n;
-    uint32_t* keys_sorted = ids + n;
-    uint32_t* sorted = keys_sorted + n;
-    e = launch_zero_words(out, n_pad, stream);  // padding slots [n, n_pad) hold 0
+hipError_t launch_slot_sort(const uint8_t* codes, int64_t n, int m, int lanes, void* scratch, size_t scratch_bytes,
+                            const uint32_t** counts, hipStream_t stream) {
+    if (n <= 0 || m <= 0 || m > 64 || n > (int64_t{1} << 31) - 1 || (lanes != 16 && lanes != 32 && lanes != 64))
+        return hipErrorInvalidValue;
+    ScratchParts sp;
+    hipError_t e = scratch_parts(scratch, scratch_bytes, n, m, &sp);
     if (e != hipSuccess) return e;
     const int64_t grid = std::min<int64_t>((n + 255) / 256, 65535);
-    hipLaunchKernelGGL(slot_keys_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream, codes, n, m, keys,
-                       ids);
+    hipLaunchKernelGGL(slot_keys_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream, codes, n, m, sp.keys,
+                       sp.ids);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    e = hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, keys_sorted, ids, sorted, static_cast<int>(n), 0,
-                                           32, stream);
+    e = hipcub::DeviceRadixSort::SortPairs(sp.temp, sp.temp_bytes, sp.keys, sp.keys_sorted, sp.ids, sp.sorted,
+                                           static_cast<int>(n), 0, 32, stream);
+    if (e != hipSuccess) return e;
+    e = launch_zero_words(sp.counts, static_cast<int64_t>(m) * kRows * kRows, stream);
+    if (e != hipSuccess) return e;
+    const int64_t full = n / kBlockSlots;
+    const int64_t samples = static_cast<int64_t>(order::sample_count(static_cast<size_t>(full)));
+    if (samples > 0) {
+        if (lanes == 16)
+            hipLaunchKernelGGL(cooccurrence_kernel<16>, dim3(static_cast<unsigned>(samples)), dim3(256), 0, stream,
+                               codes, m, sp.sorted, full, samples, sp.counts);
+        else if (lanes == 32)
+            hipLaunchKernelGGL(cooccurrence_kernel<32>, dim3(static_cast<unsigned>(samples)), dim3(256), 0, stream,
+                               codes, m, sp.sorted, full, samples, sp.counts);
+        else
+            hipLaunchKernelGGL(cooccurrence_kernel<64>, dim3(static_cast<unsigned>(samples)), dim3(256), 0, stream,
+                               codes, m, sp.sorted, full, samples, sp.counts);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    *counts = sp.counts;
+    return hipSuccess;
+}
+
+hipError_t launch_slot_place(const uint8_t* codes, int64_t n, int m, int64_t n_pad, int lanes, void* scratch,
+                             size_t scratch_bytes, const uint8_t* rows, uint32_t* out, hipStream_t stream) {
+    if (n <= 0 || m <= 0 || m > 64 || n > (int64_t{1} << 31) - 1 || n_pad < n ||
+        (lanes != 16 && lanes != 32 && lanes != 64))
+        return hipErrorInvalidValue;
+    ScratchParts sp;
+    hipError_t e = scratch_parts(scratch, scratch_bytes, n, m, &sp);
+    if (e != hipSuccess) return e;
+    e = launch_zero_words(out, n_pad, stream);  // padding slots [n, n_pad) hold 0
     if (e != hipSuccess) return e;
     const int64_t blocks = (n + kBlockSlots - 1) / kBlockSlots;
     const int64_t tiles = n / kBlockSlots * (kBlockSlots / 64);
     const int64_t stride = static_cast<int64_t>(order::spread_stride(static_cast<size_t>(tiles)));
-    switch (m) {
-        case 16: return launch_order_blocks<16>(codes, n, m, sorted, blocks, tiles, stride, out, stream);
-        case 32: return launch_order_blocks<32>(codes, n, m, sorted, blocks, tiles, stride, out, stream);
-        case 64: return launch_order_blocks<64>(codes, n, m, sorted, blocks, tiles, stride, out, stream);
-        default: return launch_order_blocks<0>(codes, n, m, sorted, blocks, tiles, stride, out, stream);
-    }
+    if (lanes == 16) return launch_order_blocks_m<16>(codes, n, m, sp.sorted, rows, blocks, tiles, stride, out, stream);
+    if (lanes == 32) return launch_order_blocks_m<32>(codes, n, m, sp.sorted, rows, blocks, tiles, stride, out, stream);
+    return launch_order_blocks_m<64>(codes, n, m, sp.sorted, rows, blocks, tiles, stride, out, stream);
 }
 
 }  // namespace vk
