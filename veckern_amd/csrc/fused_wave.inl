@@ -666,10 +666,10 @@ __global__ void __launch_bounds__(T)
     // need the registers for their accumulators (four queries, sorted codes, slab-aligned blocks: 1M x nq=1000
     // +4.5 % with the prefetch, 10M +3.6 %).
     constexpr bool kPrefetch = !IVF && QS == 1 && M == 16;
-    // Several code words per tile in a 1024-thread block (128 VGPRs): loading all U tiles' words at the step's start
-    // spilled the later tiles' words to scratch in every step (m=32, k=100: 1 GB of scratch writes per search), so
-    // each tile's words are loaded as the tile before it starts.
-    constexpr bool kStagedWords = !IVF && M >= 32 && T == 1024;
+    // Several code words per tile, or two tables, in a 1024-thread block (128 VGPRs): loading all U tiles' words at
+    // the step's start spilled the later tiles' words to scratch in every step (m=32, k=100: 1 GB of scratch writes
+    // per search), so each tile's words are loaded as the tile before it starts.
+    constexpr bool kStagedWords = !IVF && T == 1024 && (M >= 32 || NG > 1);
     uint4 next_words[kPrefetch ? U : 1];
     SlotIds<U> next_ids;
 
@@ -887,9 +887,9 @@ __global__ void __launch_bounds__(T)
                     // The reads are issued in batches of 16 (16 / NG sub-spaces), each batch before its adds: 16
                     // reads in flight per wave, in 64 VGPRs at most (four-query entries). Left to itself the scheduler
                     // either hoists every read of a tile (eight queries: 128 VGPRs, spilled) or, with the sums fenced
-                    // before the offers, waits for each read before issuing the next. Two-register lists in a
-                    // 1024-thread block (128 VGPRs) take batches of 8: with 16 the read addresses spilled.
-                    constexpr int kBatch = (S > 1 && T == 1024 ? 8 : 16) / NG;
+                    // before the offers, waits for each read before issuing the next. Two-register lists or two
+                    // tables in a 1024-thread block (128 VGPRs) take batches of 8: with 16 the read addresses spilled.
+                    constexpr int kBatch = ((S > 1 || NG > 1) && T == 1024 ? 8 : 16) / NG;
                     static_for<0, 16 / kBatch>([&](auto bc) {
                         constexpr int b = decltype(bc)::value;
                         V v[kBatch * NG];
