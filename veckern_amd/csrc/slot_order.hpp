@@ -54,7 +54,8 @@ constexpr int kEntries = 256;   // table rows per sub-space
 
 // Lanes served together by one pass of a table read, and the number of bank groups: 64 banks of 4 bytes return
 // 256 bytes per clock, so a pass holds 256 / (entry bytes) lanes (16-byte entries: 16 lanes, 8-byte: 32, 4-byte:
-// 64) and an entry's bank group is its table row mod that count.
+// 64) and an entry's bank group is its table row mod that count. 2-byte entries (fp16 tables, one query) are taken
+// as 4-byte ones: there two rows share each bank word, which this model does not separate.
 inline int pass_lanes(int entry_bytes) { return entry_bytes >= 16 ? 16 : entry_bytes >= 8 ? 32 : 64; }
 
 // Runs f(t) for t in [0, threads) on host threads (inline when threads <= 1).
