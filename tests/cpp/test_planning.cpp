@@ -216,17 +216,20 @@ CASE("slot order: slots [0, n) hold every vector once, blocks sorted by code byt
                 }
                 EXPECT(once);
                 // Sorted slot t sits at slot spread_slot(t): tiles of the full blocks spread, the partial block in
-                // place. Taken in sorted order block by block, every vector of a later block sorts at or after
-                // every vector of an earlier one (dealing only permutes within a block).
+                // place. Taken in sorted order unit by unit (pools of pool_blocks full blocks, then single blocks),
+                // every vector of a later unit sorts at or after every vector of an earlier one (dealing only
+                // permutes within a unit).
                 auto key = [&](size_t v) { return (uint32_t(codes[v * m]) << 24) | (uint32_t(codes[v * m + 1]) << 16) |
                                                   (uint32_t(codes[v * m + 2]) << 8) | codes[v * m + 3]; };
                 const size_t tiles = n / 256 * 4, stride = vk::order::spread_stride(tiles);
+                const vk::order::Units units(n, vk::order::pool_blocks(m, lanes));
                 std::vector<char> used(n, 0);
                 bool bijective = true, sorted = true;
                 uint32_t prev_max = 0;
-                for (size_t b0 = 0; b0 < n; b0 += 256) {
+                for (size_t u = 0; u < units.count; ++u) {
+                    const size_t b0 = units.unit_block(u) * 256, b1 = b0 + units.unit_size(u) * 256;
                     uint32_t lo = UINT32_MAX, hi = 0;
-                    for (size_t t = b0; t < std::min(n, b0 + 256); ++t) {
+                    for (size_t t = b0; t < std::min(n, b1); ++t) {
                         const size_t at = vk::order::spread_slot(t, tiles, stride);
                         bijective = bijective && at < n && !used[at];
                         if (at >= n) continue;
@@ -235,7 +238,7 @@ CASE("slot order: slots [0, n) hold every vector once, blocks sorted by code byt
                         lo = std::min(lo, k);
                         hi = std::max(hi, k);
                     }
-                    sorted = sorted && (b0 == 0 || prev_max <= lo);
+                    sorted = sorted && (u == 0 || prev_max <= lo);
                     prev_max = hi;
                 }
                 EXPECT(bijective);
@@ -244,6 +247,27 @@ CASE("slot order: slots [0, n) hold every vector once, blocks sorted by code byt
                 for (size_t slot = n; slot < n_pad; ++slot) pad_zero = pad_zero && ids[vk::order::interleaved(slot)] == 0;
                 EXPECT(pad_zero);
             }
+}
+
+CASE("slot order: dealing pools fit the GPU builder's LDS budget; units cover every block once") {
+    EXPECT(vk::order::pool_blocks(16, 16) == 4 && vk::order::pool_blocks(32, 16) == 2 && vk::order::pool_blocks(64, 16) == 1);
+    EXPECT(vk::order::pool_blocks(64, 32) == 2 && vk::order::pool_blocks(32, 32) == 4 && vk::order::pool_blocks(48, 32) == 2);
+    for (size_t m : {size_t{16}, size_t{32}, size_t{48}, size_t{64}})
+        for (int lanes : {16, 32, 64}) {
+            const int pool = vk::order::pool_blocks(m, lanes);
+            EXPECT(vk::order::pool_lds_bytes(m, lanes, pool) <= vk::order::kPoolLdsBytes && 256 * pool / lanes <= 64);
+        }
+    for (size_t n : {size_t{1}, size_t{255}, size_t{256}, size_t{1023}, size_t{1024}, size_t{5 * 256 + 3}, size_t{9 * 256}})
+        for (int pool : {1, 2, 4}) {
+            const vk::order::Units units(n, pool);
+            std::vector<int> hits((n + 255) / 256, 0);
+            for (size_t u = 0; u < units.count; ++u)
+                for (size_t b = 0; b < units.unit_size(u); ++b) ++hits[units.unit_block(u) + b];
+            bool once = true;
+            for (int h : hits) once = once && h == 1;
+            EXPECT(once);
+            for (size_t u = 0; u < units.pools; ++u) EXPECT((units.unit_block(u) + pool) * 256 <= n);  // pools are full
+        }
 }
 
 CASE("slot order: the spread stride is coprime with the tile count and near its golden section") {

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "slot_order.hpp"
 
@@ -61,43 +63,55 @@ __global__ void __launch_bounds__(256) cooccurrence_kernel(const uint8_t* __rest
     }
 }
 
-// One 256-slot block per wave (order::order_blocks): the block's code rows are gathered into LDS. Its sorted
-// passes' statistics (order::block_stats: the sum over (pass, sub-space) of the largest bank-group count of distinct
-// entries, and the number of distinct entries) are taken by filling the passes in slot order with the same
-// bookkeeping the dealing keeps: `present[s * 256 + e]` (bit p: pass p reads entry e of sub-space s),
-// `count[(s * L + g) * P + p]` (pass p's distinct entries in group g of sub-space s) and `top[s * P + p]` (the
-// largest such count), lane s updating sub-space s. If the block reads at least kDealMinDistinct * m distinct
-// entries, its vectors are dealt (order::deal_block: lane (p, s-group) sums pass p's cost over its sub-spaces, the
-// wave picks the cheapest pass with room, lowest first on ties), and the dealt order is kept if its load is lower.
-// The block's ids are then written at their spread, interleaved slots. Partial last block: ids in sorted order.
-template <int M, int L>
-__global__ void __launch_bounds__(64) order_blocks_kernel(const uint8_t* __restrict__ codes, int64_t n, int m,
-                                                            const uint32_t* __restrict__ sorted,
-                                                            const uint8_t* __restrict__ table_rows, int64_t blocks,
-                                                            int64_t tiles, int64_t stride, uint32_t* __restrict__ out) {
+// Entry masks of a unit's passes: one bit per pass.
+template <int PASSES>
+using PassMask = std::conditional_t<(PASSES <= 16), uint16_t, std::conditional_t<(PASSES <= 32), uint32_t, uint64_t>>;
+
+// One dealing unit per wave (order::order_units): POOL full blocks, or one block (the units past the pools). The
+// unit's code rows are gathered into LDS. Its sorted passes' statistics (order::block_stats: the sum over (pass,
+// sub-space) of the largest bank-group count of distinct entries, and the number of distinct entries) are taken by
+// filling the passes in slot order with the same bookkeeping the dealing keeps: `present[s * 256 + e]` (bit p: pass p
+// reads entry e of sub-space s), `count[(s * L + g) * P + p]` (pass p's distinct entries in group g of sub-space s)
+// and `top[s * P + p]` (the largest such count), lane s updating sub-space s. If the unit reads at least
+// kDealMinDistinct * m distinct entries per block, its vectors are dealt (order::deal_block: lane (p, s-group) sums
+// pass p's cost over its sub-spaces, the wave picks the cheapest pass with room, lowest first on ties), and the dealt
+// order is kept if its load is lower. The unit's ids are then written at their spread, interleaved slots. The
+// partial last block: ids in sorted order.
+template <int M, int L, int POOL>
+__global__ void __launch_bounds__(64) order_units_kernel(const uint8_t* __restrict__ codes, int64_t n, int m,
+                                                           const uint32_t* __restrict__ sorted,
+                                                           const uint8_t* __restrict__ table_rows, int64_t pools,
+                                                           int64_t rest_first, int64_t units, int64_t tiles,
+                                                           int64_t stride, uint32_t* __restrict__ out) {
     constexpr int MM = M ? M : 64;  // LDS sized for the largest m when m is not fixed (m <= 64)
-    constexpr int P = kBlockSlots / L;
+    constexpr int kMaxSlots = kBlockSlots * POOL;
+    constexpr int kMaxPasses = kMaxSlots / L;  // at most 64
+    static_assert(kMaxPasses <= 64, "a pass mask holds at most 64 passes");
+    using Mask = PassMask<kMaxPasses>;
     constexpr unsigned kRaise = L > 16 ? 2u : 0u;  // order::raise_penalty(L)
-    __shared__ uint8_t rows[kBlockSlots * MM];
+    __shared__ uint8_t rows[kMaxSlots * MM];
     __shared__ uint8_t group[MM * kRows];
-    __shared__ uint16_t present[MM * kRows];
-    __shared__ uint8_t count[MM * L * P];
-    __shared__ uint8_t top[MM * P];
-    __shared__ uint8_t dealt[kBlockSlots];
+    __shared__ Mask present[MM * kRows];
+    __shared__ uint8_t count[MM * L * kMaxPasses];
+    __shared__ uint8_t top[MM * kMaxPasses];
+    __shared__ uint16_t dealt[kMaxSlots];
     const int lane = threadIdx.x;
     const int mm = M ? M : m;
-    const int64_t blk = blockIdx.x;
-    if (blk >= blocks) return;
+    const int64_t u = blockIdx.x;
+    if (u >= units) return;
+    const int64_t blk = u < pools ? u * POOL : rest_first + (u - pools);
+    const int slots = u < pools ? kMaxSlots : kBlockSlots;
+    const int P = slots / L;  // passes of this unit
     const int64_t b0 = blk * kBlockSlots;
-    const int cnt = static_cast<int>(min<int64_t>(kBlockSlots, n - b0));
+    const int cnt = static_cast<int>(min<int64_t>(slots, n - b0));
     const uint32_t* block = sorted + b0;
     auto place = [&](int64_t t) {
         const int64_t slot = t < tiles * 64 ? (t / 64) * stride % tiles * 64 + t % 64 : t;
         return (slot / 64 / 4) * 256 + (slot % 64) * 4 + (slot / 64) % 4;
     };
     bool use_dealt = false;
-    if (cnt == kBlockSlots) {
-        for (int e = lane; e < kBlockSlots * mm; e += WAVE) rows[e] = codes[static_cast<int64_t>(block[e / mm]) * mm + e % mm];
+    if (cnt == slots) {
+        for (int e = lane; e < slots * mm; e += WAVE) rows[e] = codes[static_cast<int64_t>(block[e / mm]) * mm + e % mm];
         for (int e = lane; e < mm * kRows; e += WAVE) group[e] = static_cast<uint8_t>(table_rows[e] % L);
         auto reset = [&] {
             for (int e = lane; e < mm * kRows; e += WAVE) present[e] = 0;
@@ -109,9 +123,9 @@ __global__ void __launch_bounds__(64) order_blocks_kernel(const uint8_t* __restr
             if (lane >= mm) return 0u;
             const int s = lane;
             const unsigned e = rows[i * mm + s];
-            const uint16_t mask = present[s * kRows + e];
+            const Mask mask = present[s * kRows + e];
             if ((mask >> p) & 1u) return 0u;
-            present[s * kRows + e] = static_cast<uint16_t>(mask | (1u << p));
+            present[s * kRows + e] = static_cast<Mask>(mask | (Mask{1} << p));
             const int c = ++count[(s * L + group[s * kRows + e]) * P + p];
             if (c > top[s * P + p]) top[s * P + p] = static_cast<uint8_t>(c);
             return 1u;
@@ -125,43 +139,58 @@ __global__ void __launch_bounds__(64) order_blocks_kernel(const uint8_t* __restr
         reset();
         __syncthreads();
         unsigned distinct = 0;
-        for (int i = 0; i < kBlockSlots; ++i) distinct += add(i, i / L);  // lane s touches sub-space s only
+        for (int i = 0; i < slots; ++i) distinct += add(i, i / L);  // lane s touches sub-space s only
         __syncthreads();
         for (int o = WAVE / 2; o > 0; o >>= 1) distinct += static_cast<unsigned>(__shfl_xor(static_cast<int>(distinct), o));
         const unsigned sorted_load = load();
-        if (distinct >= order::kDealMinDistinct * static_cast<unsigned>(mm)) {
-            __syncthreads();
-            reset();
-            __syncthreads();
-            const int p = lane % P, s0 = lane / P;  // this lane's pass and first sub-space
-            int fill = 0;                          // lanes of pass p: vectors dealt to pass p so far
-            for (int i = 0; i < kBlockSlots; ++i) {
+        // The dealing, with the unit's pass count PP a compile-time constant (the cost loop then unrolls over a
+        // fixed m and keeps its table reads in flight together).
+        auto deal = [&](auto pc) {
+            constexpr int PP = decltype(pc)::value;
+            const int p = lane % PP, s0 = lane / PP;  // this lane's pass and first sub-space
+            constexpr int kStep = WAVE / PP;
+            int fill = 0;                            // lanes of pass p: vectors dealt to it so far
+            for (int i = 0; i < PP * L; ++i) {
                 const uint8_t* row = rows + i * mm;
-                unsigned cost = 0;
-                for (int s = s0; s < mm; s += WAVE / P) {
+                auto cost_of = [&](int s) {
                     const unsigned e = row[s];
-                    if ((present[s * kRows + e] >> p) & 1u) continue;
-                    const unsigned c = count[(s * L + group[s * kRows + e]) * P + p];
-                    const unsigned t = top[s * P + p];
-                    cost += c + (c + 1u > (t > 1u ? t : 1u) ? kRaise : 0u);
+                    const unsigned c = count[(s * L + group[s * kRows + e]) * PP + p];
+                    const unsigned t = top[s * PP + p];
+                    const bool there = (present[s * kRows + e] >> p) & 1u;
+                    return there ? 0u : c + (c + 1u > (t > 1u ? t : 1u) ? kRaise : 0u);
+                };
+                unsigned cost = 0;
+                if constexpr (M > 0) {
+#pragma unroll
+                    for (int k = 0; k < (M + kStep - 1) / kStep; ++k)
+                        if (s0 + k * kStep < M) cost += cost_of(s0 + k * kStep);
+                } else {
+                    for (int s = s0; s < mm; s += kStep) cost += cost_of(s);
                 }
 #pragma unroll
-                for (int o = P; o < WAVE; o <<= 1) cost += static_cast<unsigned>(__shfl_xor(static_cast<int>(cost), o));
+                for (int o = PP; o < WAVE; o <<= 1) cost += static_cast<unsigned>(__shfl_xor(static_cast<int>(cost), o));
                 // Cheapest pass with room, lowest pass on ties: the minimum of (cost, pass) over passes with room.
-                unsigned key = fill < L ? (cost << 4) | static_cast<unsigned>(p) : 0xffffffffu;
+                unsigned key = fill < L ? (cost << 6) | static_cast<unsigned>(p) : 0xffffffffu;
 #pragma unroll
-                for (int o = 1; o < P; o <<= 1) {
+                for (int o = 1; o < PP; o <<= 1) {
                     const unsigned other = static_cast<unsigned>(__shfl_xor(static_cast<int>(key), o));
                     key = other < key ? other : key;
                 }
-                const int best = static_cast<int>(key & 15u);
+                const int best = static_cast<int>(key & 63u);
                 const int at = __shfl(fill, best);  // the best pass's fill before this vector (lane best: pass best)
                 __syncthreads();                    // every lane has read present / count / top for this vector
                 add(i, best);
-                if (lane == 0) dealt[best * L + at] = static_cast<uint8_t>(i);
+                if (lane == 0) dealt[best * L + at] = static_cast<uint16_t>(i);
                 if (p == best) ++fill;
                 __syncthreads();
             }
+        };
+        if (distinct >= order::kDealMinDistinct * static_cast<unsigned>(mm) * static_cast<unsigned>(slots / kBlockSlots)) {
+            __syncthreads();
+            reset();
+            __syncthreads();
+            if (slots == kMaxSlots) deal(std::integral_constant<int, kMaxPasses>{});
+            else deal(std::integral_constant<int, kBlockSlots / L>{});
             use_dealt = load() < sorted_load;
         }
     }
@@ -169,22 +198,35 @@ __global__ void __launch_bounds__(64) order_blocks_kernel(const uint8_t* __restr
     for (int j = lane; j < cnt; j += WAVE) out[place(b0 + j)] = block[use_dealt ? dealt[j] : j];
 }
 
-template <int M, int L>
-hipError_t launch_order_blocks(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, const uint8_t* rows,
-                               int64_t blocks, int64_t tiles, int64_t stride, uint32_t* out, hipStream_t stream) {
-    hipLaunchKernelGGL((order_blocks_kernel<M, L>), dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream, codes,
-                       n, m, sorted, rows, blocks, tiles, stride, out);
+template <int M, int L, int POOL>
+hipError_t launch_order_units(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, const uint8_t* rows,
+                              const order::Units& un, int64_t tiles, int64_t stride, uint32_t* out,
+                              hipStream_t stream) {
+    hipLaunchKernelGGL((order_units_kernel<M, L, POOL>), dim3(static_cast<unsigned>(un.count)), dim3(64), 0, stream,
+                       codes, n, m, sorted, rows, static_cast<int64_t>(un.pools), static_cast<int64_t>(un.rest_first),
+                       static_cast<int64_t>(un.count), tiles, stride, out);
     return hipGetLastError();
 }
 
+// The instance of the pool order::pool_blocks gives for this m (fixed, or up to 64) and pass width.
+template <int M, int L>
+hipError_t launch_order_units_pool(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted,
+                                   const uint8_t* rows, const order::Units& un, int64_t tiles, int64_t stride,
+                                   uint32_t* out, hipStream_t stream) {
+    constexpr int kPool = order::pool_blocks(M ? M : 64, L);  // m not fixed: sized as m = 64, like pool_blocks
+    if (static_cast<int>(un.pool) != kPool) return hipErrorInvalidValue;
+    return launch_order_units<M, L, kPool>(codes, n, m, sorted, rows, un, tiles, stride, out, stream);
+}
+
 template <int L>
-hipError_t launch_order_blocks_m(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, const uint8_t* rows,
-                                 int64_t blocks, int64_t tiles, int64_t stride, uint32_t* out, hipStream_t stream) {
+hipError_t launch_order_units_m(const uint8_t* codes, int64_t n, int m, const uint32_t* sorted, const uint8_t* rows,
+                                const order::Units& un, int64_t tiles, int64_t stride, uint32_t* out,
+                                hipStream_t stream) {
     switch (m) {
-        case 16: return launch_order_blocks<16, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
-        case 32: return launch_order_blocks<32, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
-        case 64: return launch_order_blocks<64, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
-        default: return launch_order_blocks<0, L>(codes, n, m, sorted, rows, blocks, tiles, stride, out, stream);
+        case 16: return launch_order_units_pool<16, L>(codes, n, m, sorted, rows, un, tiles, stride, out, stream);
+        case 32: return launch_order_units_pool<32, L>(codes, n, m, sorted, rows, un, tiles, stride, out, stream);
+        case 64: return launch_order_units_pool<64, L>(codes, n, m, sorted, rows, un, tiles, stride, out, stream);
+        default: return launch_order_units_pool<0, L>(codes, n, m, sorted, rows, un, tiles, stride, out, stream);
     }
 }
 
@@ -273,12 +315,12 @@ hipError_t launch_slot_place(const uint8_t* codes, int64_t n, int m, int64_t n_p
     if (e != hipSuccess) return e;
     e = launch_zero_words(out, n_pad, stream);  // padding slots [n, n_pad) hold 0
     if (e != hipSuccess) return e;
-    const int64_t blocks = (n + kBlockSlots - 1) / kBlockSlots;
     const int64_t tiles = n / kBlockSlots * (kBlockSlots / 64);
     const int64_t stride = static_cast<int64_t>(order::spread_stride(static_cast<size_t>(tiles)));
-    if (lanes == 16) return launch_order_blocks_m<16>(codes, n, m, sp.sorted, rows, blocks, tiles, stride, out, stream);
-    if (lanes == 32) return launch_order_blocks_m<32>(codes, n, m, sp.sorted, rows, blocks, tiles, stride, out, stream);
-    return launch_order_blocks_m<64>(codes, n, m, sp.sorted, rows, blocks, tiles, stride, out, stream);
+    const order::Units units(static_cast<size_t>(n), order::pool_blocks(static_cast<size_t>(m), lanes));
+    if (lanes == 16) return launch_order_units_m<16>(codes, n, m, sp.sorted, rows, units, tiles, stride, out, stream);
+    if (lanes == 32) return launch_order_units_m<32>(codes, n, m, sp.sorted, rows, units, tiles, stride, out, stream);
+    return launch_order_units_m<64>(codes, n, m, sp.sorted, rows, units, tiles, stride, out, stream);
 }
 
 }  // namespace vk

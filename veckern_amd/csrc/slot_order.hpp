@@ -84,18 +84,19 @@ struct SlotOrder {
     int lanes = 16;
 };
 
-// A block's cost in the model of the reads: over its 256 / lanes passes and the m sub-spaces, `load` sums the
-// largest number of distinct entries in one bank group among a pass's lanes (about the LDS cycles of its reads, up
-// to a factor; entries read by several lanes of a pass are one broadcast), and `distinct` the numbers of distinct
-// entries. `rows` holds the block's code rows, `order` the local row of each slot, `group` the bank group of each
-// (sub-space, code).
+// The cost of `slots` slots (whole blocks) in the model of the reads: over their slots / lanes passes and the m
+// sub-spaces, `load` sums the largest number of distinct entries in one bank group among a pass's lanes (about the
+// LDS cycles of its reads, up to a factor; entries read by several lanes of a pass are one broadcast), and
+// `distinct` the numbers of distinct entries. `rows` holds the slots' code rows, `order` the local row of each
+// slot, `group` the bank group of each (sub-space, code).
 struct BlockStats {
     unsigned load = 0, distinct = 0;
 };
 template <typename Index>
-inline BlockStats block_stats(const uint8_t* rows, size_t m, const Index* order, int lanes, const uint8_t* group) {
+inline BlockStats block_stats(const uint8_t* rows, size_t m, const Index* order, int lanes, const uint8_t* group,
+                              size_t slots = kBlock) {
     BlockStats st;
-    for (int p = 0; p < static_cast<int>(kBlock) / lanes; ++p)
+    for (int p = 0; p < static_cast<int>(slots) / lanes; ++p)
         for (size_t s = 0; s < m; ++s) {
             uint64_t seen[4] = {};
             uint8_t count[64] = {};
@@ -116,32 +117,52 @@ inline BlockStats block_stats(const uint8_t* rows, size_t m, const Index* order,
 // over passes and sub-spaces, are dealt: kDealMinDistinct * m distinct (pass, sub-space) entries per block.
 constexpr unsigned kDealMinDistinct = kBlock / 2;
 
+// Consecutive full blocks dealt together (a pool): their vectors may go to any pass of the pool, which leaves the
+// dealing more choice. The pool is the largest of 4, 2, 1 blocks with at most 64 passes whose bookkeeping fits the
+// GPU builder's LDS budget (kPoolLdsBytes, sized for m rounded up to 64 when it is not 16, 32 or 64): entry masks
+// (one bit per pass), group counts, pass maxima, bank groups, the pool's code rows and its dealt order. Modelled
+// bank load (mean largest distinct-entry count per (pass, sub-space)): 100M uniform codes, 16-lane passes, 2.03 per
+// block, 1.93 in pools of 4; 1M x m=64, 32-lane passes, 2.60 per block, 2.51 in pools of 2.
+constexpr size_t kPoolLdsBytes = 120 * 1024;
+constexpr size_t pool_lds_bytes(size_t m, int lanes, int pool) {
+    const size_t mm = (m == 16 || m == 32 || m == 64) ? m : 64;
+    const size_t passes = kBlock * static_cast<size_t>(pool) / static_cast<size_t>(lanes);
+    const size_t mask = passes <= 16 ? 2 : passes <= 32 ? 4 : 8;
+    return mm * kEntries * mask + mm * kEntries * pool + mm * passes + mm * kEntries + kBlock * pool * mm +
+           2 * kBlock * pool;
+}
+constexpr int pool_blocks(size_t m, int lanes) {
+    for (int pool = 4; pool > 1; pool /= 2)
+        if (kBlock * pool / lanes <= 64 && pool_lds_bytes(m, lanes, pool) <= kPoolLdsBytes) return pool;
+    return 1;
+}
+
 // The dealing's extra cost for an entry that raises a pass's largest bank-group count: 2 for passes of 32 or 64
 // lanes, none for 16. Measured on the search kernel: 1M x m=64 (32 lanes) 4.42 -> 4.34 ms with it; 100M uniform
 // codes (16 lanes) 99.2 -> 99.8 ms, so 16-lane passes go without.
 inline unsigned raise_penalty(int lanes) { return lanes > 16 ? 2u : 0u; }
 
-// Deals one full block's vectors (local rows 0..255, in sorted order) to its passes; `out` receives local rows in
-// slot order (pass p holds slots p * lanes ..). One vector at a time goes to the pass with room where it costs
-// least, the lowest pass on ties. Its cost in a pass sums, over the sub-spaces whose entry the pass does not read
-// yet, the entries the pass already reads in that entry's bank group, plus raise_penalty(lanes) if the entry would
-// raise the pass's largest group count above max(that count, 1). Scratch: `present[s * 256 + e]`, the passes
-// (bit p) that read entry e of sub-space s; `count[(s * lanes + g) * passes + p]`, pass p's distinct entries in
-// group g of sub-space s; `top[s * passes + p]`, the largest of those over g.
-inline void deal_block(const uint8_t* rows, size_t m, int lanes, const uint8_t* group, uint8_t* out,
-                       std::vector<uint16_t>& present, std::vector<uint8_t>& count, std::vector<uint8_t>& top) {
-    const int passes = static_cast<int>(kBlock) / lanes;
+// Deals the vectors of `slots` slots (whole blocks; local rows 0..slots-1, in sorted order) to their passes; `out`
+// receives local rows in slot order (pass p holds slots p * lanes ..). One vector at a time goes to the pass with
+// room where it costs least, the lowest pass on ties. Its cost in a pass sums, over the sub-spaces whose entry the
+// pass does not read yet, the entries the pass already reads in that entry's bank group, plus raise_penalty(lanes)
+// if the entry would raise the pass's largest group count above max(that count, 1). Scratch: `present[s * 256 + e]`,
+// the passes (bit p) that read entry e of sub-space s; `count[(s * lanes + g) * passes + p]`, pass p's distinct
+// entries in group g of sub-space s; `top[s * passes + p]`, the largest of those over g.
+inline void deal_block(const uint8_t* rows, size_t m, int lanes, const uint8_t* group, size_t slots, uint16_t* out,
+                       std::vector<uint64_t>& present, std::vector<uint8_t>& count, std::vector<uint8_t>& top) {
+    const int passes = static_cast<int>(slots) / lanes;  // at most 64
     present.assign(m * kEntries, 0);
     count.assign(m * lanes * passes, 0);
     top.assign(m * passes, 0);
     const unsigned raise = raise_penalty(lanes);
-    int fill[16] = {};
-    for (int i = 0; i < static_cast<int>(kBlock); ++i) {
+    int fill[64] = {};
+    for (int i = 0; i < static_cast<int>(slots); ++i) {
         const uint8_t* row = rows + static_cast<size_t>(i) * m;
-        unsigned cost[16] = {};
+        unsigned cost[64] = {};
         for (size_t s = 0; s < m; ++s) {
             const unsigned e = row[s];
-            const unsigned mask = present[s * kEntries + e];
+            const uint64_t mask = present[s * kEntries + e];
             const uint8_t* c = &count[(s * lanes + group[s * kEntries + e]) * passes];
             const uint8_t* t = &top[s * passes];
             for (int p = 0; p < passes; ++p)
@@ -156,14 +177,14 @@ inline void deal_block(const uint8_t* rows, size_t m, int lanes, const uint8_t* 
             }
         for (size_t s = 0; s < m; ++s) {
             const unsigned e = row[s];
-            uint16_t& mask = present[s * kEntries + e];
+            uint64_t& mask = present[s * kEntries + e];
             if ((mask >> best) & 1u) continue;
-            mask = static_cast<uint16_t>(mask | (1u << best));
+            mask |= uint64_t{1} << best;
             uint8_t& c = count[(s * lanes + group[s * kEntries + e]) * passes + best];
             uint8_t& t = top[s * passes + best];
             t = std::max<uint8_t>(t, ++c);
         }
-        out[best * lanes + fill[best]++] = static_cast<uint8_t>(i);
+        out[best * lanes + fill[best]++] = static_cast<uint16_t>(i);
     }
 }
 
@@ -332,30 +353,48 @@ inline void mirror_counts(std::vector<uint32_t>& w, size_t m) {
     }
 }
 
-// Blocks [blk_lo, blk_hi) of the sorted ids: dealt where that pays, then written to `ids` at their spread slots. A
-// full block's code rows are first gathered into a local copy, which the statistics and the dealing then read.
-inline void order_blocks(const uint8_t* codes, size_t n, size_t m, const uint32_t* sorted, int lanes,
-                         const uint8_t* group, size_t blk_lo, size_t blk_hi, uint32_t* ids) {
+// Units of the dealing: the first full_blocks / pool * pool full blocks in pools of `pool`, then the remaining
+// blocks one at a time (the partial last block, if any, among them). Unit u starts at block unit_block(u) and holds
+// unit_size(u) blocks.
+struct Units {
+    size_t pools = 0, pool = 1, rest_first = 0, count = 0;
+    Units(size_t n, int pool_) : pool(static_cast<size_t>(pool_)) {
+        const size_t full = n / kBlock, blocks = (n + kBlock - 1) / kBlock;
+        pools = pool > 1 ? full / pool : 0;
+        rest_first = pools * pool;
+        count = pools + (blocks - rest_first);
+    }
+    size_t unit_block(size_t u) const { return u < pools ? u * pool : rest_first + (u - pools); }
+    size_t unit_size(size_t u) const { return u < pools ? pool : 1; }
+};
+
+// Units [u_lo, u_hi) of the sorted ids: a unit of full blocks is dealt where that pays (at least kDealMinDistinct * m
+// distinct entries per block, and a lower modelled load), then every slot is written to `ids` at its spread slot. A
+// unit's code rows are first gathered into a local copy, which the statistics and the dealing then read.
+inline void order_units(const uint8_t* codes, size_t n, size_t m, const uint32_t* sorted, int lanes,
+                        const uint8_t* group, const Units& units, size_t u_lo, size_t u_hi, uint32_t* ids) {
     const size_t tiles = n / kBlock * (kBlock / kTile), stride = spread_stride(tiles);
     auto place = [&](size_t t) { return interleaved(spread_slot(t, tiles, stride)); };
-    std::vector<uint8_t> local(kBlock), dealt(kBlock);
-    std::vector<uint8_t> rows(kBlock * m);
-    std::vector<uint16_t> present;
+    const size_t cap = kBlock * units.pool;
+    std::vector<uint16_t> local(cap), dealt(cap);
+    std::vector<uint8_t> rows(cap * m);
+    std::vector<uint64_t> present;
     std::vector<uint8_t> count, top;
-    for (size_t i = 0; i < kBlock; ++i) local[i] = static_cast<uint8_t>(i);
-    for (size_t blk = blk_lo; blk < blk_hi; ++blk) {
-        const size_t b0 = blk * kBlock;
-        const size_t cnt = std::min(kBlock, n - b0);
+    for (size_t i = 0; i < cap; ++i) local[i] = static_cast<uint16_t>(i);
+    for (size_t u = u_lo; u < u_hi; ++u) {
+        const size_t b0 = units.unit_block(u) * kBlock;
+        const size_t slots = units.unit_size(u) * kBlock;
+        const size_t cnt = std::min(slots, n - b0);
         const uint32_t* block = sorted + b0;
-        if (cnt == kBlock) {
-            for (size_t i = 0; i < kBlock; ++i)
+        if (cnt == slots) {
+            for (size_t i = 0; i < slots; ++i)
                 std::copy(codes + static_cast<size_t>(block[i]) * m, codes + (static_cast<size_t>(block[i]) + 1) * m,
                           rows.begin() + i * m);
-            const BlockStats st = block_stats(rows.data(), m, local.data(), lanes, group);
-            if (st.distinct >= kDealMinDistinct * m) {
-                deal_block(rows.data(), m, lanes, group, dealt.data(), present, count, top);
-                if (block_stats(rows.data(), m, dealt.data(), lanes, group).load < st.load) {
-                    for (size_t j = 0; j < kBlock; ++j) ids[place(b0 + j)] = block[dealt[j]];
+            const BlockStats st = block_stats(rows.data(), m, local.data(), lanes, group, slots);
+            if (st.distinct >= kDealMinDistinct * m * (slots / kBlock)) {
+                deal_block(rows.data(), m, lanes, group, slots, dealt.data(), present, count, top);
+                if (block_stats(rows.data(), m, dealt.data(), lanes, group, slots).load < st.load) {
+                    for (size_t j = 0; j < slots; ++j) ids[place(b0 + j)] = block[dealt[j]];
                     continue;
                 }
             }
@@ -365,8 +404,8 @@ inline void order_blocks(const uint8_t* codes, size_t n, size_t m, const uint32_
 }
 
 // The layout for table reads of `lanes` lanes per pass (pass_lanes): vectors sorted by their first four code bytes;
-// table rows fitted per sub-space to the sorted passes' co-occurrences (fit_rows); the full blocks dealt with the
-// fitted bank groups where that pays; tiles spread and ids interleaved. Work is split over up to `threads` host
+// table rows fitted per sub-space to the sorted passes' co-occurrences (fit_rows); the full blocks dealt in pools
+// (pool_blocks) with the fitted bank groups where that pays; tiles spread and ids interleaved. Work is split over up to `threads` host
 // threads.
 inline SlotOrder slot_order(const uint8_t* codes, size_t n, size_t m, size_t n_pad, int lanes, unsigned threads = 0) {
     SlotOrder o;
@@ -380,9 +419,10 @@ inline SlotOrder slot_order(const uint8_t* codes, size_t n, size_t m, size_t n_p
     o.rows = fit_all_rows(cooccurrence(codes, n, m, sorted.data(), lanes, sub_threads), m, lanes, sub_threads);
     std::vector<uint8_t> group(m * kEntries);
     for (size_t e = 0; e < group.size(); ++e) group[e] = static_cast<uint8_t>(o.rows[e] % lanes);
+    const Units units(n, pool_blocks(m, lanes));
     parallel(threads, [&](unsigned t) {
-        order_blocks(codes, n, m, sorted.data(), lanes, group.data(), blocks * t / threads,
-                     blocks * (t + 1) / threads, o.ids.data());
+        order_units(codes, n, m, sorted.data(), lanes, group.data(), units, units.count * t / threads,
+                    units.count * (t + 1) / threads, o.ids.data());
     });
     return o;
 }
