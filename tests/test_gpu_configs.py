@@ -128,8 +128,11 @@ def test_config_c_k100_all_queries(cfg, q):
     assert shape.queries_per_block == q
 
 
-def test_config_d_10m():
-    run_config("D", 4, 100)
+@pytest.mark.parametrize("q", [4, 8])
+def test_config_d_10m(q):
+    # Q=8, the benchmark's default at 10M: two 4-query tables sharing each address, code words staged per tile.
+    _, shape = run_config("D", q, 100)
+    assert shape.queries_per_block == q and shape.threads == 1024
 
 
 def test_config_d1_single_query():
