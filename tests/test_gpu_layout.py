@@ -81,3 +81,21 @@ def test_layout_rows_move_co_read_entries_apart():
         fitted = load(lambda sub, e: rows[sub, e] % 16)
         print(f"\n    bank load of the GPU layout: rows = codes {plain:.3f}, fitted rows {fitted:.3f}")
         assert fitted < 0.8 * plain
+
+
+def test_layout_beyond_64_subspaces_is_built_on_the_host():
+    # m = 128: the GPU builder's LDS sizing covers m <= 64, so the searcher builds this layout with the host
+    # definition; its tables (128 KB for one query) still fit, so the search runs at one query per block.
+    rng = np.random.default_rng(21)
+    n, d, m = 5_003, 256, 128
+    centroids = rng.standard_normal((m, 256, d // m)).astype(np.float32)
+    codes = rng.integers(0, 256, size=(n, m), dtype=np.uint8)
+    queries = rng.standard_normal((6, d)).astype(np.float32)
+    with vk.PQSearcher(centroids, codes, d) as s:
+        got_d, got_i, _ = s.search(queries, 10, vk.ScanVariant.FusedWarp)
+        assert s.last_launch().queries_per_block == 1
+        exp = orc.adc_search(centroids, d, codes, queries, 10)
+        assert np.array_equal(got_i, exp["id"]) and np.array_equal(got_d.view(np.uint32), exp["dist"].view(np.uint32))
+        ids, rows, lanes = s.layout()
+        assert lanes == 64
+        check_layout(ids, rows, n, m)
