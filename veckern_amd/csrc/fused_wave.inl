@@ -619,6 +619,16 @@ __global__ void __launch_bounds__(T)
     // LDS write (lane q: query q), always (they only fall).
     constexpr bool kLaneBound = kShareBound && QS * W <= WAVE && (W == 2 || W == 4 || W == 8 || W == 16);
     __shared__ __align__(16) unsigned rank_bound[QS][W];
+    // Admission queue of the two-register lists (K > 64, fp32 tables): candidates that pass a list's filter a few
+    // at a time are appended to a run of kQueueCap LDS slots of their (query, wave) instead of being inserted one
+    // by one (~32 VALU instructions each into a 128-entry list). A full run, a tile that admits kMergeMin or more
+    // at once, and the end of the slab go in by one bitonic merge (merge_wave). The merge keeps the K smallest
+    // pairs of the list and of everything offered to it, so the list ends as the one-by-one inserts leave it; the
+    // queued candidates were tested against a threshold that has fallen since, which only admits a few more.
+    constexpr int kQueueCap = 32;
+    constexpr int kQueueBytes = QS * W * kQueueCap * static_cast<int>(sizeof(Pair));
+    constexpr bool kQueue = !IVF && !F16 && S == 2 && M > 0 && NG * M * KSUB * E::kBytes + kQueueBytes <= 150 * 1024;
+    __shared__ Pair queue[kQueue ? QS * W * kQueueCap : 1];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
     const int words = m / 16;
@@ -657,6 +667,7 @@ __global__ void __launch_bounds__(T)
     constexpr bool kBulkOne = QS == 1 && !F16;
     WaveList<S, IVF || (!F16 && S > 1) || kBulkOne || BULK, kShareBound> lists[QS];
     float published[QS];
+    unsigned queued[QS];  // admission queue: candidates held in each list's run (wave-uniform)
     const int bound_rank = (a.K + W - 1) / W - 1;  // < 64: the entry lives in the lists' first register
     int32_t run_query = -1;                        // IVF: the query whose tables and lists are current
     // One query per block over 16-byte codes: the next granule's code words and ids are loaded before this
@@ -747,6 +758,7 @@ __global__ void __launch_bounds__(T)
                 lists[q].init();
                 if (!live[q]) lists[q].disable();
                 published[q] = INFINITY;
+                queued[q] = 0;
             }
         }
         const uint32_t n32 = static_cast<uint32_t>(a.n);  // n < 2^31: ids and tile bounds fit in 32 bits
@@ -754,6 +766,35 @@ __global__ void __launch_bounds__(T)
         // One granule step of this wave (g: the wave's granule, advanced at the end). bulk_step: candidates are
         // admitted in bulk whatever the list type.
         int64_t g = g_lo + wave;
+        // Admission queue: merges list q's queued candidates into it.
+        auto flush = [&](int q) __attribute__((always_inline)) {
+            const Pair* const run = queue + (q * W + wave) * kQueueCap;
+            const bool held = static_cast<unsigned>(lane) < queued[q];
+            Pair e{INFINITY, kEmptyId};
+            if (held) e = run[lane];
+            lists[q].merge_wave(e.d, e.i, held, a.K);
+            queued[q] = 0;
+        };
+        // Admission queue: offers this tile's candidates of query q.
+        auto queue_offer = [&](int q, float x, int32_t xi, uint64_t valid) __attribute__((always_inline)) {
+            uint64_t mask = __builtin_amdgcn_ballot_w64(x <= lists[q].filter) & valid;
+            if (!mask) return;
+            unsigned n = static_cast<unsigned>(__popcll(mask));
+            if (n >= static_cast<unsigned>(lists[q].kMergeMin)) {
+                lists[q].merge_wave(x, xi, (mask >> lane) & 1, a.K);
+                return;
+            }
+            if (queued[q] + n > static_cast<unsigned>(kQueueCap)) {
+                flush(q);
+                mask = __builtin_amdgcn_ballot_w64(x <= lists[q].filter) & valid;
+                if (!mask) return;
+                n = static_cast<unsigned>(__popcll(mask));
+            }
+            const unsigned pos = queued[q] + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+            if ((mask >> lane) & 1) queue[(q * W + wave) * kQueueCap + pos] = Pair{x, xi};
+            queued[q] += n;
+        };
         auto granule = [&](auto bulk_step) __attribute__((always_inline)) {
             // The next granule for this wave, asked for now and used after this one (inverted lists: every W-th).
             unsigned grab = 0;
@@ -954,6 +995,7 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
                 for (int q = 0; q < QS; ++q) {
                     if constexpr (decltype(bulk_step)::value) lists[q].offer_masked_bulk(acc[q], static_cast<int32_t>(id), valid, a.K);
+                    else if constexpr (kQueue) queue_offer(q, acc[q], static_cast<int32_t>(id), valid);
                     else lists[q].offer_masked(acc[q], static_cast<int32_t>(id), valid, a.K);
                 }
             }
@@ -988,6 +1030,11 @@ __global__ void __launch_bounds__(T)
             if (g < g_hi) granule(std::true_type{});
         }
         while (g < g_hi) granule(std::false_type{});
+        if constexpr (kQueue) {
+#pragma unroll
+            for (int q = 0; q < QS; ++q)
+                if (queued[q]) flush(q);
+        }
 
         // Inverted lists: when the query's run of slabs ends (or the block's range does), every wave writes its
         // list for the query at part[((b + query) * W + wave) * K]. Along the granule order both the block and the
