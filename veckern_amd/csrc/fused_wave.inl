@@ -622,7 +622,7 @@ __global__ void __launch_bounds__(T)
     // Admission queue of the wave lists (fp32 tables, static LDS): candidates that pass a list's filter a few at a
     // time are appended to a run of kQueueCap LDS slots of their (query, wave) instead of being inserted one by one
     // (~22 VALU instructions each into a one-register list, ~32 into a two-register one). A full run, a tile that
-    // admits kMergeMin or more at once, and the end of the slab go in by one bitonic merge (merge_wave). The merge
+    // admits a whole run's worth at once, and the end of the slab go in by one bitonic merge (merge_wave). The merge
     // keeps the K smallest pairs of the list and of everything offered to it, so the list ends as the one-by-one
     // inserts leave it; the queued candidates were tested against a threshold that has fallen since, which only
     // admits a few more. Measured: 1M x nq=1000 (m=16, k=10) 0.637 -> 0.605 ms per search, m=32 (k=100) VALU per
@@ -784,7 +784,7 @@ __global__ void __launch_bounds__(T)
             uint64_t mask = __builtin_amdgcn_ballot_w64(x <= lists[q].filter) & valid;
             if (!mask) return;
             unsigned n = static_cast<unsigned>(__popcll(mask));
-            if (n >= static_cast<unsigned>(lists[q].kMergeMin)) {
+            if (n >= static_cast<unsigned>(kQueueCap)) {
                 lists[q].merge_wave(x, xi, (mask >> lane) & 1, a.K);
                 return;
             }
