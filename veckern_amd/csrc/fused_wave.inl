@@ -626,13 +626,14 @@ __global__ void __launch_bounds__(T)
     // keeps the K smallest pairs of the list and of everything offered to it, so the list ends as the one-by-one
     // inserts leave it; the queued candidates were tested against a threshold that has fallen since, which only
     // admits a few more. Measured: 1M x nq=1000 (m=16, k=10) 0.637 -> 0.605 ms per search, m=32 (k=100) VALU per
-    // table read 7.18 -> 5.93 (3.5 % faster, the LDS then binding); 10M and 100M unchanged. The fp16-table kernels
+    // table read 7.18 -> 5.93 (3.5 % faster, the LDS then binding); 10M and 100M unchanged; inverted lists (flushed
+    // when a query's run of lists ends) 0.201 -> 0.190 ms at nprobe 32, 0.087 -> 0.080 at nprobe 8. The fp16-table kernels
     // have no registers for it: their 8-query loop then spilled (1M -11 %, 10M -28 %).
     constexpr int kTableBytes = NG * M * KSUB * E::kBytes;
     constexpr int kRunBytes = QS * W * static_cast<int>(sizeof(Pair));  // one slot per (query, wave)
     constexpr int kQueueCap = kTableBytes + 32 * kRunBytes <= 150 * 1024 ? 32
                               : kTableBytes + 16 * kRunBytes <= 150 * 1024 ? 16 : 0;
-    constexpr bool kQueue = !IVF && !F16 && S <= 2 && M > 0 && kQueueCap > 0;
+    constexpr bool kQueue = !F16 && S <= 2 && M > 0 && kQueueCap > 0;
     __shared__ Pair queue[kQueue ? QS * W * kQueueCap : 1];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
@@ -1035,11 +1036,15 @@ __global__ void __launch_bounds__(T)
             if (g < g_hi) granule(std::true_type{});
         }
         while (g < g_hi) granule(std::false_type{});
-        if constexpr (kQueue) {
+        // Queued candidates go into the lists before they are stored (inverted lists: at the end of a query's run).
+        auto flush_all = [&]() __attribute__((always_inline)) {
+            if constexpr (kQueue) {
 #pragma unroll
-            for (int q = 0; q < QS; ++q)
-                if (queued[q]) flush(q);
-        }
+                for (int q = 0; q < QS; ++q)
+                    if (queued[q]) flush(q);
+            }
+        };
+        if constexpr (!IVF) flush_all();
 
         // Inverted lists: when the query's run of slabs ends (or the block's range does), every wave writes its
         // list for the query at part[((b + query) * W + wave) * K]. Along the granule order both the block and the
@@ -1047,8 +1052,10 @@ __global__ void __launch_bounds__(T)
         // and a query's lists (from consecutive blocks) are contiguous for the merge kernel.
         if constexpr (IVF) {
             item = slab_next;
-            if (item >= end || item >= a.query_gran[run_query + 1])
+            if (item >= end || item >= a.query_gran[run_query + 1]) {
+                flush_all();
                 lists[0].store(a.part + ((b + run_query) * W + wave) * a.K, a.K);
+            }
             continue;
         }
 
