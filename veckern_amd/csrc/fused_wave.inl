@@ -626,9 +626,9 @@ __global__ void __launch_bounds__(T)
     // keeps the K smallest pairs of the list and of everything offered to it, so the list ends as the one-by-one
     // inserts leave it; the queued candidates were tested against a threshold that has fallen since, which only
     // admits a few more. Measured: 1M x nq=1000 (m=16, k=10) 0.637 -> 0.605 ms per search, m=32 (k=100) VALU per
-    // table read 7.18 -> 5.93 (3.5 % faster, the LDS then binding); 10M and 100M unchanged; inverted lists (flushed
-    // when a query's run of lists ends) 0.201 -> 0.190 ms at nprobe 32, 0.087 -> 0.080 at nprobe 8. The fp16-table kernels
-    // have no registers for it: their 8-query loop then spilled (1M -11 %, 10M -28 %).
+    // table read 7.18 -> 5.93 (3.5 % faster, the LDS then binding); 10M and 100M unchanged; inverted lists
+    // (flushed when a query's run of lists ends) 0.201 -> 0.190 ms at nprobe 32, 0.087 -> 0.080 at nprobe 8. The
+    // fp16-table kernels have no registers for it: their 8-query loop then spilled (1M -11 %, 10M -28 %).
     constexpr int kTableBytes = NG * M * KSUB * E::kBytes;
     constexpr int kRunBytes = QS * W * static_cast<int>(sizeof(Pair));  // one slot per (query, wave)
     constexpr int kQueueCap = kTableBytes + 32 * kRunBytes <= 150 * 1024 ? 32
