@@ -772,12 +772,16 @@ __global__ void __launch_bounds__(T)
         // One granule step of this wave (g: the wave's granule, advanced at the end). bulk_step: candidates are
         // admitted in bulk whatever the list type.
         int64_t g = g_lo + wave;
-        // Admission queue: merges list q's queued candidates into it.
+        // Admission queue: merges list q's queued candidates into it. Lanes read slots that other lanes of the wave
+        // wrote: the LDS serves one wave's accesses in order, and the wave barriers keep the compiler from moving
+        // these reads above those writes, or the next appends above these reads.
         auto flush = [&](int q) __attribute__((always_inline)) {
             const Pair* const run = queue + (q * W + wave) * kQueueCap;
             const bool held = static_cast<unsigned>(lane) < queued[q];
             Pair e{INFINITY, kEmptyId};
+            __builtin_amdgcn_wave_barrier();
             if (held) e = run[lane];
+            __builtin_amdgcn_wave_barrier();
             lists[q].merge_wave(e.d, e.i, held, a.K);
             queued[q] = 0;
         };
