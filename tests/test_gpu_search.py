@@ -205,6 +205,30 @@ def test_fused_warp_other_m_and_tie_heavy_data(family, m):
                 assert_same(got_d, got_i, exp, f"{family} m={m} Q={q} k={k}")
 
 
+def test_admission_bursts_from_falling_distances():
+    # The scan visits vectors sorted by their first code bytes. Here sub-space 0 dominates every distance and falls
+    # as its code rises, so along the scan nearly every tile beats the lists' thresholds: tiles admit a few lanes,
+    # many lanes, or all 64, the lists' admission queues fill and overflow mid-granule, and whole tiles merge at once.
+    # A small second query mixes in the usual sparse admissions. Both must equal the oracle at every list length.
+    rng = np.random.default_rng(23)
+    n, d, m, nq = 60_013, 32, 16, 11
+    dsub = d // m
+    centroids = rng.standard_normal((m, 256, dsub)).astype(np.float32)
+    centroids[0, :, 0] = np.arange(256, dtype=np.float32)
+    centroids[0, :, 1] = 0.0
+    codes = rng.integers(0, 256, size=(n, m), dtype=np.uint8)
+    queries = rng.standard_normal((nq, d)).astype(np.float32)
+    queries[: nq - 1, 0] = 1000.0  # (1000 - c)^2 falls with the sub-space-0 code c, in steps of ~1500
+    queries[:, 1] = 0.0  # the other sub-spaces add ~30 of noise, distinct values within a step
+    with vk.PQSearcher(centroids, codes, d) as s:
+        for k in (1, 10, 64, 100, 128):
+            exp = orc.adc_search(centroids, d, codes, queries, k)
+            for q in (1, 2, 4, 8):
+                s.set_tuning(vk.Tuning(queries_per_block=q))
+                got_d, got_i, _ = s.search(queries, k, vk.ScanVariant.FusedWarp)
+                assert_same(got_d, got_i, exp, f"falling k={k} Q={q}")
+
+
 def test_generic_m_path():
     # m = 48 is not one of the compile-time specialisations; the kernel reads m at run time.
     n, d, m, nq = 9_001, 96, 48, 9
