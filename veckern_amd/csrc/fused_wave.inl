@@ -634,6 +634,7 @@ __global__ void __launch_bounds__(T)
     constexpr int kQueueCap = kTableBytes + 32 * kRunBytes <= 150 * 1024 ? 32
                               : kTableBytes + 16 * kRunBytes <= 150 * 1024 ? 16 : 0;
     constexpr bool kQueue = !F16 && S <= 2 && M > 0 && kQueueCap > 0;
+    static_assert(kQueueCap <= WAVE / 2, "a flush merges at most half a wave of queued candidates");
     __shared__ Pair queue[kQueue ? QS * W * kQueueCap : 1];
     unsigned char* const tables = reinterpret_cast<unsigned char*>(M ? lds_static : lds_dynamic);
     const int m = M ? M : a.m;
@@ -777,12 +778,12 @@ __global__ void __launch_bounds__(T)
         // these reads above those writes, or the next appends above these reads.
         auto flush = [&](int q) __attribute__((always_inline)) {
             const Pair* const run = queue + (q * W + wave) * kQueueCap;
-            const bool held = static_cast<unsigned>(lane) < queued[q];
+            const bool held = lane >= WAVE / 2 && static_cast<unsigned>(lane - WAVE / 2) < queued[q];
             Pair e{INFINITY, kEmptyId};
             __builtin_amdgcn_wave_barrier();
-            if (held) e = run[lane];
+            if (held) e = run[lane - WAVE / 2];
             __builtin_amdgcn_wave_barrier();
-            lists[q].merge_wave(e.d, e.i, held, a.K);
+            lists[q].merge_upper_half(e.d, e.i, held, a.K);
             queued[q] = 0;
         };
         // Admission queue: offers this tile's candidates of query q.
