@@ -624,9 +624,8 @@ __global__ void __launch_bounds__(T)
     // (~22 VALU instructions each into a one-register list, ~32 into a two-register one). A full run and the end of
     // the slab go in by one bitonic merge from the upper half-wave (merge_upper_half), a tile that admits a whole
     // run's worth at once by one from all its lanes (merge_wave). A merge keeps the K smallest pairs of the list and
-    // of everything offered to it, so the list ends as the one-by-one
-    // inserts leave it; the queued candidates were tested against a threshold that has fallen since, which only
-    // admits a few more. Measured: 1M x nq=1000 (m=16, k=10) 0.637 -> 0.605 ms per search, m=32 (k=100) VALU per
+    // of everything offered to it, so the list ends as the one-by-one inserts leave it; the queued candidates were
+    // tested against a threshold that has fallen since, which only admits a few more. Measured: 1M x nq=1000 (m=16, k=10) 0.637 -> 0.605 ms per search, m=32 (k=100) VALU per
     // table read 7.18 -> 5.93 (3.5 % faster, the LDS then binding); 10M and 100M unchanged; inverted lists
     // (flushed when a query's run of lists ends) 0.201 -> 0.190 ms at nprobe 32, 0.087 -> 0.080 at nprobe 8. The
     // fp16-table kernels have no registers for it: their 8-query loop then spilled (1M -11 %, 10M -28 %).
