@@ -1063,8 +1063,8 @@ struct vk_ivf {
     hipStream_t stream = nullptr;
     DeviceBuffer<float> coarse, centroids, queries, lut, coarse_dist;
     DeviceBuffer<uint4> codes_v;
-    DeviceBuffer<int32_t> ids, slab_list, slab_queries;
-    DeviceBuffer<int64_t> list_tile, slab_gran, query_gran;
+    DeviceBuffer<int32_t> ids, slab_queries;
+    DeviceBuffer<int64_t> list_tile, slab_tile, slab_gran, query_gran;
     DeviceBuffer<Pair> probes, part, out;
     PinnedBuffer<float> staged_q;  // host-buffer searches: queries and results staged in page-locked memory
     PinnedBuffer<Pair> staged_out;
@@ -1092,12 +1092,12 @@ struct vk_ivf {
         // 2. the slab plan, on the device: slabs in query-major order (each query's probed lists in probe order),
         // so a query's slabs are one run of consecutive granules
         const size_t slabs = nq * nprobe;
-        slab_list.ensure(slabs);
+        slab_tile.ensure(slabs);
         slab_queries.ensure(slabs);
         slab_gran.ensure(slabs + 1);
         query_gran.ensure(nq + 1);
         vk::IvfPlanArgs plan{probes.get(),      static_cast<int>(nprobe), static_cast<int64_t>(nq), list_tile.get(),
-                             slab_list.get(),   slab_queries.get(),       slab_gran.get(),           query_gran.get()};
+                             slab_tile.get(),   slab_queries.get(),       slab_gran.get(),           query_gran.get()};
         clock.time(&t->lut_ms, [&] {
             for (size_t r0 = 0; r0 < nq; r0 += rows) {
                 const size_t nr = std::min(rows, nq - r0);
@@ -1158,7 +1158,7 @@ struct vk_ivf {
         a.part = part.get();
         a.n_slabs = static_cast<int64_t>(slabs);
         a.slab_gran = slab_gran.get();
-        a.slab_list = slab_list.get();
+        a.slab_tile = slab_tile.get();
         a.slab_queries = slab_queries.get();
         a.query_gran = query_gran.get();
         a.list_tile = list_tile.get();

@@ -576,11 +576,12 @@ __device__ __forceinline__ int64_t slab_of(const int64_t* slab_gran, int64_t sla
     return lo;
 }
 
-// IVF (one query per slab, QS = 1): the scan runs over inverted lists. Slab s is list a.slab_list[s] probed by
-// query a.slab_queries[s]; slabs are in query-major order, so a query's probed lists form one run of consecutive
-// slabs, granules [a.query_gran[q], a.query_gran[q + 1]) of the balanced partition (a.query_gran[nq] = total).
-// Slab s covers granules [a.slab_gran[s], a.slab_gran[s + 1]) (possibly none), its list's padded tiles start at
-// a.list_tile[list] in the word-interleaved codes, and the vector ids come from a.ids (-1 on padding). A block
+// IVF (one query per slab, QS = 1): the scan runs over inverted lists. Slab s is a list probed by query
+// a.slab_queries[s]; slabs are in query-major order, so a query's probed lists form one run of consecutive slabs,
+// granules [a.query_gran[q], a.query_gran[q + 1]) of the balanced partition (a.query_gran[nq] = total). Slab s covers
+// granules [a.slab_gran[s], a.slab_gran[s + 1]) (possibly none), its list's padded tiles start at a.slab_tile[s] in
+// the word-interleaved codes (the plan copies the list's first tile there, one dependent load fewer per slab than
+// looking it up by list), and the vector ids come from a.ids (-1 on padding). A block
 // gathers a query's tables and starts its lists once per run and writes them once, at the end of the run (or of
 // its range); a separate merge kernel combines the partial lists of each query.
 template <int QG, int NG, int U, int M, int S, int T, bool F16, bool IVF, bool BULK>
@@ -733,7 +734,7 @@ __global__ void __launch_bounds__(T)
             }
         }
         int64_t list_tile0 = 0;  // IVF: first tile of the slab's list
-        if constexpr (IVF) list_tile0 = a.list_tile[a.slab_list[slab]];
+        if constexpr (IVF) list_tile0 = a.slab_tile[slab];
         if constexpr (kPrefetch) {
             if (g_lo + wave < g_hi) {
                 const uint4* c = a.codes + (g_lo + wave) * U * WAVE + lane;

@@ -48,19 +48,19 @@ __global__ void __launch_bounds__(kPlanThreads) ivf_plan_runs_kernel(IvfPlanArgs
     int64_t run = 0;
     for (int base = 0; base < a.nprobe; base += WAVE) {
         const int p = base + lane;
-        int32_t list = 0;
+        int64_t tile = 0;
         int64_t gran = 0;
         if (p < a.nprobe) {
             const int32_t l = a.probes[q * a.nprobe + p].i;
             if (l >= 0) {  // a query whose coarse distances are all NaN probes nothing
-                list = l;
-                gran = (a.list_tile[l + 1] - a.list_tile[l]) / 4;
+                tile = a.list_tile[l];
+                gran = (a.list_tile[l + 1] - tile) / 4;
             }
         }
         const int64_t incl = wave_inclusive_sum(gran);
         if (p < a.nprobe) {
             const int64_t s = q * a.nprobe + p;
-            a.slab_list[s] = list;
+            a.slab_tile[s] = tile;
             a.slab_queries[s] = static_cast<int32_t>(q);
             a.slab_gran[s] = run + incl - gran;
         }

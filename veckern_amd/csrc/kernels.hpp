@@ -67,7 +67,7 @@ struct WaveScanArgs {
     // `max_slots` are then unused (the total is query_gran[nq]).
     int64_t n_slabs;
     const int64_t* slab_gran;      // [n_slabs + 1] granule prefix of the slabs
-    const int32_t* slab_list;      // [n_slabs] list scanned by each slab
+    const int64_t* slab_tile;      // [n_slabs] first tile in `codes` / `ids` of the list each slab scans
     const int32_t* slab_queries;   // [n_slabs] query of each slab; a query's slabs are consecutive
     const int64_t* query_gran;     // [nq + 1] granule prefix of the queries' runs of slabs
     const int64_t* list_tile;      // [lists + 1] first tile of each list in `codes` / `ids`
@@ -91,7 +91,8 @@ WaveScanKernel fused_wave_kernel(int qg, int ng, int ilp, int m, int segments, b
 WaveScanKernel ivf_kernel(int m, int segments);
 
 // ---- IVF plan (ivf.hip): from the probes (nq x nprobe, id -1 = no list), slab q * nprobe + p = query q's p-th
-// probed list: slab_list / slab_queries [nq * nprobe], slab_gran [nq * nprobe + 1] (granule starts; a probe of no
+// probed list: slab_tile (the list's first tile) / slab_queries [nq * nprobe], slab_gran [nq * nprobe + 1] (granule
+// starts; a probe of no
 // list or of an empty list is an empty slab), query_gran [nq + 1] (the granule start of each query's run; the last
 // entry is the total).
 struct IvfPlanArgs {
@@ -99,7 +100,7 @@ struct IvfPlanArgs {
     int nprobe;
     int64_t nq;
     const int64_t* list_tile;
-    int32_t* slab_list;
+    int64_t* slab_tile;
     int32_t* slab_queries;
     int64_t* slab_gran;
     int64_t* query_gran;
