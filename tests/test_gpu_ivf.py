@@ -75,6 +75,16 @@ def test_ivf_blocks_finish_many_queries():
             assert ix.last_launch().blocks_x < 3_000 * 2
 
 
+def test_ivf_plan_with_many_slabs():
+    # 3000 queries x 32 probes = 96,000 slabs (the plan's prefix over queries runs in one block, its slab offsets in
+    # one thread per slab), against 3000 x 2.
+    coarse, cent, codes, list_ids, queries = ivf_case(97, 20_000, 32, 16, 3_000, 200)
+    with vk.IVFIndex(coarse, cent, codes, list_ids) as ix:
+        for nprobe in (32, 2):
+            d, i, _ = ix.search(queries, nprobe, 10)
+            assert_same(d, i, orc.ivf_search(coarse, cent, 32, codes, list_ids, queries, nprobe, 10), f"nprobe={nprobe}")
+
+
 def test_ivf_single_query_spreads_lists_over_many_blocks(index_case):
     (coarse, cent, codes, list_ids, queries), ix = index_case
     ix.set_tuning(vk.Tuning(queries_per_block=4))
